@@ -1,0 +1,226 @@
+"""MLA decode benchmark on one MI355X (BASELINE metric: B=64, H=128, L=4096 bf16).
+
+A step is one decode call over the whole batch with inputs resident in HBM and the tile
+schedule computed beforehand (it is computed once per decode step and shared by every
+layer).  Prints ONE JSON line with the metric, the roofline of the dominant kernel (the
+split-KV main kernel, timed with HIP events on the launch stream) and the CPU oracle
+timed on the host cores as a baseline.
+
+    python bench.py [--steps K] [--warmup W] [--config C2] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+MFMA_PEAK_TFLOPS = 2500.0   # dense bf16 / fp16
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="C2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline")
+    ap.add_argument("--all-configs", action="store_true", help="also print one line per config to stderr")
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def time_gpu(fn, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per call
+
+
+def measure(cfg_name, steps, warmup):
+    import torch
+    from mlc_decode_amd import _lib
+    from mlc_decode_amd.api import flash_mla_with_kvcache, get_mla_metadata
+    from mlc_decode_amd.inputs import CONFIGS, algorithmic_bytes, algorithmic_flops, make_inputs
+
+    cfg = CONFIGS[cfg_name]
+    cpu_inp = make_inputs(cfg, seed=0)
+    inp = cpu_inp.to("cuda:0")
+    B, s_q, H = cfg.batch, cfg.s_q, cfg.heads
+    stream = torch.cuda.current_stream()
+    forced = cfg.num_splits or 0
+    sched, splits = get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=forced)
+    out = torch.empty(B, s_q, H, 512, dtype=cfg.dtype, device="cuda:0")
+    lse = torch.empty(B, H, s_q, dtype=torch.float32, device="cuda:0")
+
+    def call():
+        flash_mla_with_kvcache(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, 512,
+                               sched, splits, softmax_scale=inp.sm_scale, causal=inp.causal,
+                               out=out, lse=lse)
+
+    # whole call: main split-KV kernel + combine
+    ms_call = time_gpu(call, steps, warmup, stream)
+
+    # combine alone, re-run on the partials the last call left in the workspace
+    import ctypes
+    from mlc_decode_amd.api import workspace
+    from mlc_decode_amd._lib import MlaDecodeArgs, check
+    lib = _lib.load()
+    ws_bytes = lib.mla_workspace_bytes(B, s_q, H, sched.shape[0])
+    ws = workspace(inp.q.device, ws_bytes)
+    a = MlaDecodeArgs()
+    a.batch, a.s_q, a.heads_q, a.heads_k, a.dtype = B, s_q, H, 1, 0 if cfg.dtype == torch.bfloat16 else 1
+    a.causal, a.sm_scale, a.num_blocks = int(inp.causal), inp.sm_scale, inp.kv_cache.shape[0]
+    a.q_nope, a.q_rope = inp.q.data_ptr(), inp.q.data_ptr() + 1024
+    a.q_stride_b, a.q_stride_s, a.q_stride_h = inp.q.stride(0), inp.q.stride(1), inp.q.stride(2)
+    a.q_rope_stride_b, a.q_rope_stride_s, a.q_rope_stride_h = a.q_stride_b, a.q_stride_s, a.q_stride_h
+    a.kv_nope, a.kv_rope = inp.kv_cache.data_ptr(), inp.kv_cache.data_ptr() + 1024
+    a.kv_stride_page = a.kv_rope_stride_page = inp.kv_cache.stride(0)
+    a.kv_stride_tok = a.kv_rope_stride_tok = inp.kv_cache.stride(1)
+    a.block_table, a.block_table_stride = inp.block_table.data_ptr(), inp.block_table.stride(0)
+    a.num_parts = sched.shape[0]
+    a.cache_seqlens, a.tile_sched, a.num_splits = inp.cache_seqlens.data_ptr(), sched.data_ptr(), splits.data_ptr()
+    a.out, a.lse = out.data_ptr(), lse.data_ptr()
+    a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride(0), out.stride(1), out.stride(2)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
+    sp = stream.cuda_stream
+    ms_combine = time_gpu(lambda: check("mla_combine_fwd", lib.mla_combine_fwd(ctypes.byref(a), sp)),
+                          steps, warmup, stream)
+    ms_meta = time_gpu(lambda: get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=forced),
+                       steps, warmup, stream)
+    ms_main = max(ms_call - ms_combine, 1e-6)
+
+    nbytes = algorithmic_bytes(cpu_inp.cache_seqlens, B, s_q, H, 2)
+    flops = algorithmic_flops(cpu_inp.cache_seqlens, s_q, H, cfg.causal)
+    t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+    t_mfma = flops / (MFMA_PEAK_TFLOPS * 1e12)
+    bound = "hbm" if t_hbm >= t_mfma else "mfma"
+    gbs = nbytes / (ms_main * 1e-3) / 1e9
+    tflops = flops / (ms_main * 1e-3) / 1e12
+    n_splits = int(splits[-1].item())
+    return dict(cfg=cfg, cpu_inp=cpu_inp, ms_call=ms_call, ms_main=ms_main, ms_combine=ms_combine,
+                ms_meta=ms_meta, nbytes=nbytes, flops=flops, bound=bound, gbs=gbs, tflops=tflops,
+                parts=int(sched.shape[0]), n_splits=n_splits)
+
+
+def cpu_baseline(m, budget_s):
+    """The fp32 CPU oracle (the reference's torch decode, restated in oracle/) on a bounded
+    sample of the same workload's sequences, scaled to microseconds per full call."""
+    import torch
+    from oracle import mla_ref as R
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    inp = m["cpu_inp"]
+    B = inp.q.shape[0]
+    idx = [0]
+    R.decode_paged(inp.q[:1], inp.kv_cache, inp.block_table[:1], inp.cache_seqlens[:1],
+                   inp.sm_scale, inp.causal)  # warm-up
+    t0 = time.perf_counter()
+    R.decode_paged(inp.q[:1], inp.kv_cache, inp.block_table[:1], inp.cache_seqlens[:1],
+                   inp.sm_scale, inp.causal)
+    per_seq = max(time.perf_counter() - t0, 1e-6)
+    n = max(1, min(B, int(budget_s / 3 / per_seq)))
+    idx = list(range(n))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        R.decode_paged(inp.q[idx], inp.kv_cache, inp.block_table[idx], inp.cache_seqlens[idx],
+                       inp.sm_scale, inp.causal)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[1]
+    tok_sample = int(inp.cache_seqlens[idx].sum())
+    tok_all = int(inp.cache_seqlens.sum())
+    us_full = med * 1e6 * tok_all / max(tok_sample, 1)
+    return {"value": round(us_full, 1), "unit": "us/call", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{n} of {B} sequences ({tok_sample} of {tok_all} cached tokens), median of 3, "
+                      f"scaled by token count; fp32 torch on {cpu_model()}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    m = measure(args.config, args.steps, args.warmup)
+    cfg = m["cfg"]
+    if args.all_configs:
+        for name in ("C1", "C2", "C3", "C4", "C5"):
+            mm = m if name == args.config else measure(name, max(20, args.steps // 4), 5)
+            print(json.dumps({"config": name, "us_call": round(mm["ms_call"] * 1e3, 2),
+                              "us_main": round(mm["ms_main"] * 1e3, 2),
+                              "us_combine": round(mm["ms_combine"] * 1e3, 2),
+                              "tbps": round(mm["gbs"] / 1e3, 3), "tflops": round(mm["tflops"], 1),
+                              "bound": mm["bound"], "parts": mm["parts"], "splits": mm["n_splits"]}),
+                  file=sys.stderr, flush=True)
+    peak = HBM_PEAK_GBS if m["bound"] == "hbm" else MFMA_PEAK_TFLOPS
+    achieved = m["gbs"] if m["bound"] == "hbm" else m["tflops"]
+    traffic = None
+    tfile = os.path.join(REPO, "profiles", f"traffic_{args.config}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    line = {
+        "metric": "MLA decode us/call (B=64,H=128,L=4096)",
+        "value": round(m["ms_call"] * 1e3, 3),
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(m["ms_call"], 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp16",
+        "data": "synthetic (seeded N(0,1) q and paged latent cache, random block table)",
+        "config": {"workload": f"{cfg.name}: MLA decode B={cfg.batch} s_q={cfg.s_q} H={cfg.heads} "
+                               f"d_qk=576 d_v=512 page=64", "batch": cfg.batch, "s_q": cfg.s_q,
+                   "heads": cfg.heads, "seq_len": cfg.seqlen, "parts": m["parts"],
+                   "splits": m["n_splits"]},
+        "hbm_tbps": round(m["gbs"] / 1e3, 3),
+        "mfma_tflops": round(m["tflops"], 2),
+        "main_kernel_us": round(m["ms_main"] * 1e3, 3),
+        "combine_us": round(m["ms_combine"] * 1e3, 3),
+        "metadata_us": round(m["ms_meta"] * 1e3, 3),
+        "roofline": {"bound": m["bound"], "achieved": round(achieved, 2), "peak": peak,
+                     "unit": "GB/s" if m["bound"] == "hbm" else "TFLOP/s",
+                     "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "algorithmic_bytes": m["nbytes"], "algorithmic_flops": m["flops"]},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(m, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

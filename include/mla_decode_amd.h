@@ -1,0 +1,200 @@
+/*
+ * mla_decode_amd.h -- C ABI of the MI355X (gfx950) MLA decode library.
+ *
+ * Multi-head latent attention decode against one shared latent KV head:
+ *   q        [B, s_q, H, 576]   (512 latent "nope" dims + 64 rope dims)
+ *   kv cache [num_blocks, 64, 1, 576] paged, V = the first 512 dims of K
+ *   out      [B, s_q, H, 512],  lse [B, H, s_q] fp32 (natural log)
+ *
+ * Every buffer is caller-owned device memory; every entry point takes an
+ * explicit stream and returns 0 on success or a nonzero MLA_ERR_* code, with
+ * a message readable through mla_last_error() on the calling thread.  Nothing
+ * here allocates device memory: the split-KV workspace is sized by
+ * mla_workspace_bytes() and passed in.
+ *
+ * Reference interfaces each entry point replaces (paths are relative to the
+ * reference repository NiseAzaka/mlc_decode):
+ *   - mla_launch            handmade/mla_handmade.py:34-52 (extern "C" mla_launch)
+ *   - mla_get_metadata      the get_mla_metadata call of handmade/bench_metax_flashmla.py:31
+ *                           (algorithm described in docs/num_split_design.md:31-135)
+ *   - mla_decode_fwd        the flash_mla_with_kvcache call of handmade/bench_metax_flashmla.py:33-35,
+ *                           and the main + combine TileLang kernels of mla_decode.py:78-259
+ *   - mla_combine_fwd       the combine kernel of mla_decode.py:194-246 (LSE-weighted merge)
+ *   - mla_split_plan        _split_plan of mla_decode.py:9-30
+ */
+#ifndef MLA_DECODE_AMD_H
+#define MLA_DECODE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLA_DECODE_AMD_VERSION 1
+
+/* dtypes of q / kv / out */
+#define MLA_DTYPE_BF16 0
+#define MLA_DTYPE_F16 1
+
+/* status codes */
+#define MLA_OK 0
+#define MLA_ERR_INVALID 1   /* bad shape, stride, pointer alignment or dtype */
+#define MLA_ERR_WORKSPACE 2 /* workspace missing or too small */
+#define MLA_ERR_HIP 3       /* a HIP runtime call failed (launch error etc.) */
+#define MLA_ERR_UNSUPPORTED 4
+
+/* Fixed geometry of the latent cache. */
+#define MLA_DIM_QK 576
+#define MLA_DIM_V 512
+#define MLA_PAGE_TOKENS 64
+/* Each part of the tile schedule is described by this many int32 words. */
+#define MLA_SCHED_WORDS 8
+
+/*
+ * Decode arguments.  Strides are in elements.  The latent ("nope", dims
+ * 0..511) and rope (dims 512..575) halves may live in one tensor (rope pointer
+ * = latent pointer + 512, same strides) or in two tensors.
+ *
+ * KV addressing:
+ *   block_table != NULL (paged):  token t of sequence b lives in page
+ *     p = block_table[b * block_table_stride + t / 64], row t % 64:
+ *     latent at kv_nope + p*kv_stride_page + (t%64)*kv_stride_tok
+ *     rope   at kv_rope + p*kv_rope_stride_page + (t%64)*kv_rope_stride_tok
+ *   block_table == NULL (contiguous, the reference's [B, L, 1, D] layout):
+ *     latent at kv_nope + b*kv_stride_batch + t*kv_stride_tok (rope alike).
+ * q element (b, s, h, d) is at q_nope + b*q_stride_b + s*q_stride_s + h*q_stride_h + d
+ * (d < 512) or q_rope + b*q_rope_stride_b + s*q_rope_stride_s + h*q_rope_stride_h + (d - 512).
+ * lse may be NULL (not written).
+ * Alignment: q/kv base pointers 16-byte aligned and their strides multiples of 8 elements;
+ * out 8-byte aligned with strides multiples of 4; workspace 256-byte aligned.
+ * out element (b, s, h, d) is at out + b*o_stride_b + s*o_stride_s + h*o_stride_h + d.
+ * lse is a contiguous fp32 [B, H, s_q] array (natural log of the softmax denominator
+ * of sm_scale * q.k); rows with no visible key get out = 0 and lse = -inf.
+ */
+typedef struct mla_decode_args {
+  int32_t batch;
+  int32_t s_q;
+  int32_t heads_q;
+  int32_t heads_k; /* must be 1 (one shared latent head) */
+  int32_t dtype;   /* MLA_DTYPE_BF16 or MLA_DTYPE_F16 */
+  int32_t causal;  /* s_q > 1: query i sees keys [0, L - s_q + i] */
+  float sm_scale;
+  int32_t num_blocks; /* pool size of the paged cache (page ids are clamped to it) */
+
+  const void* q_nope;
+  const void* q_rope;
+  int64_t q_stride_b, q_stride_s, q_stride_h;
+  int64_t q_rope_stride_b, q_rope_stride_s, q_rope_stride_h;
+
+  const void* kv_nope;
+  const void* kv_rope;
+  int64_t kv_stride_page, kv_stride_tok, kv_stride_batch;
+  int64_t kv_rope_stride_page, kv_rope_stride_tok, kv_rope_stride_batch;
+
+  const int32_t* block_table; /* [B, block_table_stride] int32 or NULL */
+  int32_t block_table_stride;
+  int32_t num_parts;            /* rows of tile_sched */
+  const int32_t* cache_seqlens; /* [B] int32 (device) */
+  const int32_t* tile_sched;    /* [num_parts, MLA_SCHED_WORDS] from mla_get_metadata */
+  const int32_t* num_splits;    /* [B + 1] prefix sums from mla_get_metadata */
+
+  void* out;
+  int64_t o_stride_b, o_stride_s, o_stride_h;
+  float* lse;
+
+  void* workspace;
+  int64_t workspace_bytes;
+} mla_decode_args;
+
+/* Library version (MLA_DECODE_AMD_VERSION). */
+int mla_version(void);
+
+/* Message for the last nonzero status returned on this thread ("" if none). */
+const char* mla_last_error(void);
+
+/*
+ * Number of schedule parts the decode kernel is laid out for on a device with
+ * cu_count compute units (cu_count <= 0: query the current device).
+ * Replaces the num_sm_parts rule described in docs/num_split_design.md:53-71.
+ */
+int mla_num_parts(int32_t batch, int32_t s_q, int32_t heads_q, int32_t heads_k, int32_t cu_count);
+
+/*
+ * Tile schedule on the device (one tiny kernel on `stream`).
+ * cache_seqlens: [B] int32; tile_sched: [num_parts, 8] int32 out; num_splits: [B+1] int32 out.
+ * forced_splits <= 0: balanced greedy packing over num_parts parts (every part gets about
+ *   total/num_parts 64-token pages plus a fixed per-split overhead of fixed_overhead pages;
+ *   fixed_overhead < 0 selects the built-in default).
+ * forced_splits > 0: every sequence is cut into min(forced_splits, pages) contiguous
+ *   near-equal page ranges (the spread family of mla_decode.py:9-30); then
+ *   num_parts must equal batch * forced_splits.
+ * Replaces get_mla_metadata (handmade/bench_metax_flashmla.py:31).
+ */
+int mla_get_metadata(const int32_t* cache_seqlens, int32_t batch, int32_t num_parts,
+                     int32_t fixed_overhead, int32_t forced_splits, int32_t* tile_sched,
+                     int32_t* num_splits, void* stream);
+
+/* The same schedule computed on the host from host arrays (no GPU needed). */
+int mla_get_metadata_host(const int32_t* cache_seqlens, int32_t batch, int32_t num_parts,
+                          int32_t fixed_overhead, int32_t forced_splits, int32_t* tile_sched,
+                          int32_t* num_splits);
+
+/* Workspace bytes mla_decode_fwd needs for this problem and part count. */
+int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t num_parts);
+
+/*
+ * Split-KV decode: main kernel (one workgroup per (schedule part, head block))
+ * followed by the LSE combine for sequences cut into more than one split.
+ * Replaces flash_mla_with_kvcache (handmade/bench_metax_flashmla.py:33-35) and the
+ * TileLang main + combine kernels (mla_decode.py:78-259).
+ */
+int mla_decode_fwd(const mla_decode_args* args, void* stream);
+
+/*
+ * Combine stage alone, over partials produced by mla_decode_fwd into `workspace`
+ * (run by mla_decode_fwd itself; exposed for testing and for callers that fuse
+ * the split and merge differently).  Replaces mla_decode.py:194-246.
+ */
+int mla_combine_fwd(const mla_decode_args* args, void* stream);
+
+/*
+ * Stand-alone LSE merge of explicit partials: for each (b, row) with
+ * n = num_splits[b+1] - num_splits[b] splits at slots num_splits[b] .. +n-1:
+ *   part_o  [slots, rows, 512] fp32 (each split's softmax-normalised output)
+ *   part_lse[slots, rows] fp32 (log2 of each split's softmax denominator)
+ * writes out [B, rows, 512] (dtype) and lse [B, rows] fp32 natural log, rows = s_q*heads
+ * laid out (s, h).  Sequences with n == 1 are copied through.  Follows mla_decode.py:194-246.
+ */
+int mla_merge_partials(const float* part_o, const float* part_lse, const int32_t* num_splits,
+                       int32_t batch, int32_t rows, int32_t dtype, void* out, float* lse_out,
+                       void* stream);
+
+/*
+ * The reference's split rule (mla_decode.py:9-30): spread == 0 (even family) or 1
+ * (whole-wave family).  Writes the effective split count, blocks per split and
+ * number of splits taking one extra block.  Host-only, pure integer.
+ */
+int mla_split_plan(int32_t seqlen_kv, int32_t num_split, int32_t block_n, int32_t spread,
+                   int32_t* ns_out, int32_t* blocks_per_split_out, int32_t* extra_out);
+
+/*
+ * Flat-argument launch for the reference's contiguous layout, mirroring
+ * handmade/mla_handmade.py:34-52 (mla_launch(Q, Qpe, KV, Kpe, glse, partial, out, ns)):
+ *   Q [B,H,512], Qpe [B,H,64], KV [B,L,1,512], Kpe [B,L,1,64], out [B,H,512] (dtype),
+ *   cache_seqlens [B] int32 (device), tile_sched / num_splits from mla_get_metadata,
+ *   workspace of mla_workspace_bytes(B, 1, H, num_parts) bytes.  sm_scale = 576^-0.5.
+ * The reference's glse / partial buffers are the workspace here.
+ */
+int mla_launch(const void* q, const void* q_pe, const void* kv, const void* k_pe, void* out,
+               int32_t batch, int32_t heads, int32_t kv_ctx, int32_t dtype,
+               const int32_t* cache_seqlens, const int32_t* tile_sched, int32_t num_parts,
+               const int32_t* num_splits, void* workspace, int64_t workspace_bytes,
+               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLA_DECODE_AMD_H */

@@ -1,0 +1,18 @@
+"""MI355X (gfx950) split-KV MLA decode behind the reference's Python entry points.
+
+The hot path is hand-written HIP (``csrc/mla_decode.hip``) reached through the C ABI of
+``include/mla_decode_amd.h``; this package is the torch-side host code around it.
+"""
+from .api import (flash_mla_with_kvcache, get_mla_metadata, get_mla_metadata_host,
+                  merge_partials, mla_decode_with_kvcache, num_parts_for)
+from .legacy import MlaKernel
+
+__all__ = [
+    "flash_mla_with_kvcache",
+    "get_mla_metadata",
+    "get_mla_metadata_host",
+    "merge_partials",
+    "mla_decode_with_kvcache",
+    "num_parts_for",
+    "MlaKernel",
+]

@@ -1,0 +1,257 @@
+"""Paged MLA decode on MI355X: the torch-facing entry points.
+
+* ``get_mla_metadata(cache_seqlens, num_heads_per_head_k, num_heads_k)`` ->
+  ``(tile_scheduler_metadata, num_splits)``, the call the reference makes at
+  handmade/bench_metax_flashmla.py:31 (schedule algorithm described in
+  docs/num_split_design.md:31-135), computed on the GPU by ``mla_get_metadata``.
+* ``flash_mla_with_kvcache(q, k_cache, block_table, cache_seqlens, head_dim_v,
+  tile_scheduler_metadata, num_splits, softmax_scale=None, causal=False)`` -> ``(out, lse)``,
+  the call at handmade/bench_metax_flashmla.py:33-35.
+* ``mla_decode_with_kvcache(q, kv_cache, block_table, cache_seqlens, num_splits=None,
+  sm_scale=None, causal=True)`` -> ``(out, lse)``: one call that schedules and decodes.
+
+Tensors live on the GPU; every call goes through the C ABI of ``include/mla_decode_amd.h``
+on torch's current stream.  Shapes: q ``[B, s_q, H, 576]``, kv cache ``[num_blocks, 64, 1,
+576]`` (or a ``(latent [.., 512], rope [.., 64])`` pair of views), block_table ``[B, P]``
+int32, cache_seqlens ``[B]`` int32, out ``[B, s_q, H, 512]`` in q's dtype and lse
+``[B, H, s_q]`` fp32 (natural log).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import threading
+from typing import Optional, Sequence, Tuple, Union
+
+import torch
+
+from . import _lib
+from ._lib import MLA_DIM_QK, MLA_DIM_V, MLA_DTYPE_BF16, MLA_DTYPE_F16, MlaDecodeArgs, check
+
+_DTYPES = {torch.bfloat16: MLA_DTYPE_BF16, torch.float16: MLA_DTYPE_F16}
+
+_ws_lock = threading.Lock()
+_workspaces: dict = {}
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (the decode runs only as HIP kernels)")
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A cached, 256-byte-aligned device workspace of at least ``nbytes`` bytes.
+
+    Kept per device and grown on demand, so steady-state calls allocate nothing.  Calls
+    that share a device share the buffer; they must be ordered on one stream.
+    """
+    nbytes = max(int(nbytes), 256)
+    key = (device.type, device.index)
+    with _ws_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+            _workspaces[key] = buf
+    off = (-buf.data_ptr()) % 256
+    return buf[off:off + nbytes]
+
+
+def num_parts_for(batch: int, s_q: int, heads_q: int, heads_k: int = 1, cu_count: int = 0) -> int:
+    """Schedule parts the decode kernel is laid out for (``mla_num_parts``)."""
+    n = _lib.load().mla_num_parts(batch, s_q, heads_q, heads_k, cu_count)
+    if n < 1:
+        check("mla_num_parts", -n)
+    return n
+
+
+def get_mla_metadata(cache_seqlens: torch.Tensor, num_heads_per_head_k: int, num_heads_k: int,
+                     num_parts: Optional[int] = None, fixed_overhead: int = -1,
+                     forced_splits: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Tile schedule: ``(tile_scheduler_metadata [num_parts, 8] int32, num_splits [B+1] int32)``.
+
+    ``num_heads_per_head_k`` is ``s_q * h_q // h_kv`` as in the reference's call; it picks
+    the kernel's row blocking and hence the part count.  ``forced_splits > 0`` cuts every
+    sequence into that many near-equal page ranges instead of balancing (then
+    ``num_parts = B * forced_splits``).
+    """
+    _require_gpu(cache_seqlens, "cache_seqlens")
+    if num_heads_k != 1:
+        raise ValueError("only one latent KV head (num_heads_k == 1) is supported")
+    if cache_seqlens.dtype != torch.int32 or cache_seqlens.dim() != 1:
+        raise ValueError("cache_seqlens must be a 1-D int32 tensor")
+    seqlens = cache_seqlens.contiguous()
+    batch = seqlens.numel()
+    if forced_splits > 0:
+        num_parts = batch * forced_splits
+    elif num_parts is None:
+        num_parts = num_parts_for(batch, 1, num_heads_per_head_k, 1)
+    sched = torch.empty(num_parts, _lib.MLA_SCHED_WORDS, dtype=torch.int32, device=seqlens.device)
+    splits = torch.empty(batch + 1, dtype=torch.int32, device=seqlens.device)
+    check("mla_get_metadata", _lib.load().mla_get_metadata(
+        seqlens.data_ptr(), batch, num_parts, fixed_overhead, forced_splits, sched.data_ptr(),
+        splits.data_ptr(), _stream_ptr(seqlens.device)))
+    return sched, splits
+
+
+def get_mla_metadata_host(cache_seqlens: Sequence[int], num_parts: int, fixed_overhead: int = -1,
+                          forced_splits: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The same schedule computed by the library on the host (no GPU needed)."""
+    seqlens = torch.as_tensor(list(cache_seqlens), dtype=torch.int32).contiguous()
+    batch = seqlens.numel()
+    if forced_splits > 0:
+        num_parts = batch * forced_splits
+    sched = torch.zeros(num_parts, _lib.MLA_SCHED_WORDS, dtype=torch.int32)
+    splits = torch.zeros(batch + 1, dtype=torch.int32)
+    p32 = lambda t: ctypes.cast(t.data_ptr(), ctypes.POINTER(ctypes.c_int32))  # noqa: E731
+    check("mla_get_metadata_host", _lib.load().mla_get_metadata_host(
+        p32(seqlens), batch, num_parts, fixed_overhead, forced_splits, p32(sched), p32(splits)))
+    return sched, splits
+
+
+def _split_kv(kv_cache) -> Tuple[torch.Tensor, torch.Tensor]:
+    if isinstance(kv_cache, (tuple, list)):
+        latent, rope = kv_cache
+        if latent.shape[-1] != MLA_DIM_V or rope.shape[-1] != MLA_DIM_QK - MLA_DIM_V:
+            raise ValueError("kv pair must be (latent [..., 512], rope [..., 64])")
+        return latent, rope
+    if kv_cache.shape[-1] != MLA_DIM_QK:
+        raise ValueError(f"kv_cache last dim must be {MLA_DIM_QK}")
+    return kv_cache[..., :MLA_DIM_V], kv_cache[..., MLA_DIM_V:]
+
+
+def _decode(q: torch.Tensor, kv_cache, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
+            sched: torch.Tensor, splits: torch.Tensor, sm_scale: float, causal: bool,
+            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+    _require_gpu(q, "q")
+    if q.dim() != 4 or q.shape[-1] != MLA_DIM_QK:
+        raise ValueError(f"q must be [B, s_q, H, {MLA_DIM_QK}]")
+    if q.dtype not in _DTYPES:
+        raise ValueError("q must be bfloat16 or float16")
+    latent, rope = _split_kv(kv_cache)
+    for t, n in ((latent, "kv latent"), (rope, "kv rope")):
+        _require_gpu(t, n)
+        if t.dtype != q.dtype:
+            raise ValueError("kv cache dtype must match q")
+        if t.dim() != 4 or t.shape[1] != _lib.MLA_PAGE_TOKENS or t.shape[2] != 1 or t.stride(-1) != 1:
+            raise ValueError("kv cache must be [num_blocks, 64, 1, D] with unit stride in D")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be a [B, P] int32 tensor with unit column stride")
+    if cache_seqlens.dtype != torch.int32 or cache_seqlens.dim() != 1:
+        raise ValueError("cache_seqlens must be a 1-D int32 tensor")
+    B, s_q, H, _ = q.shape
+    if block_table.shape[0] != B or cache_seqlens.shape[0] != B or splits.numel() != B + 1:
+        raise ValueError("batch size of q, block_table, cache_seqlens and num_splits disagree")
+    if q.stride(-1) != 1:
+        raise ValueError("q must have unit stride in its last dim")
+    if out is None:
+        out = torch.empty(B, s_q, H, MLA_DIM_V, dtype=q.dtype, device=q.device)
+    if lse is None:
+        lse = torch.empty(B, H, s_q, dtype=torch.float32, device=q.device)
+    if lse.shape != (B, H, s_q) or not lse.is_contiguous() or lse.dtype != torch.float32:
+        raise ValueError("lse must be a contiguous fp32 [B, H, s_q] tensor")
+    seqlens = cache_seqlens.contiguous()
+    sched = sched.contiguous()
+    splits = splits.contiguous()
+    num_parts = sched.shape[0]
+    lib = _lib.load()
+    ws_bytes = lib.mla_workspace_bytes(B, s_q, H, num_parts)
+    ws = workspace(q.device, ws_bytes)
+    el = q.element_size()
+    a = MlaDecodeArgs()
+    a.batch, a.s_q, a.heads_q, a.heads_k = B, s_q, H, 1
+    a.dtype = _DTYPES[q.dtype]
+    a.causal = 1 if causal else 0
+    a.sm_scale = float(sm_scale)
+    a.num_blocks = latent.shape[0]
+    a.q_nope = q.data_ptr()
+    a.q_rope = q.data_ptr() + MLA_DIM_V * el
+    a.q_stride_b, a.q_stride_s, a.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    a.q_rope_stride_b, a.q_rope_stride_s, a.q_rope_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    a.kv_nope, a.kv_rope = latent.data_ptr(), rope.data_ptr()
+    a.kv_stride_page, a.kv_stride_tok, a.kv_stride_batch = latent.stride(0), latent.stride(1), 0
+    a.kv_rope_stride_page, a.kv_rope_stride_tok, a.kv_rope_stride_batch = rope.stride(0), rope.stride(1), 0
+    a.block_table = block_table.data_ptr()
+    a.block_table_stride = block_table.stride(0)
+    a.num_parts = num_parts
+    a.cache_seqlens = seqlens.data_ptr()
+    a.tile_sched = sched.data_ptr()
+    a.num_splits = splits.data_ptr()
+    a.out = out.data_ptr()
+    a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride(0), out.stride(1), out.stride(2)
+    a.lse = lse.data_ptr()
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws_bytes
+    check("mla_decode_fwd", lib.mla_decode_fwd(ctypes.byref(a), _stream_ptr(q.device)))
+    return out, lse
+
+
+def flash_mla_with_kvcache(q: torch.Tensor, k_cache, block_table: torch.Tensor,
+                           cache_seqlens: torch.Tensor, head_dim_v: int,
+                           tile_scheduler_metadata: torch.Tensor, num_splits: torch.Tensor,
+                           softmax_scale: Optional[float] = None, causal: bool = False,
+                           out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+    """Paged decode with a precomputed schedule -> ``(out [B,s_q,H,512], lse [B,H,s_q])``.
+
+    Same call shape as the reference's use of FlashMLA (handmade/bench_metax_flashmla.py:33-35).
+    """
+    if head_dim_v != MLA_DIM_V:
+        raise ValueError(f"head_dim_v must be {MLA_DIM_V}")
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** -0.5
+    return _decode(q, k_cache, block_table, cache_seqlens, tile_scheduler_metadata, num_splits,
+                   softmax_scale, causal, out, lse)
+
+
+def mla_decode_with_kvcache(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
+                            cache_seqlens: torch.Tensor,
+                            num_splits: Union[None, int, Tuple[torch.Tensor, torch.Tensor]] = None,
+                            sm_scale: Optional[float] = None, causal: bool = True,
+                            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+    """Schedule + decode in one call -> ``(out, lse)``.
+
+    ``num_splits``: ``None`` = balanced schedule for this GPU; an ``int`` = cut every
+    sequence into that many page ranges (1 = the reference's serial baseline); or a
+    ``(tile_scheduler_metadata, num_splits)`` pair from :func:`get_mla_metadata`.
+    """
+    if sm_scale is None:
+        sm_scale = MLA_DIM_QK ** -0.5
+    if isinstance(num_splits, tuple):
+        sched, splits = num_splits
+    else:
+        forced = int(num_splits) if num_splits is not None else 0
+        if num_splits is not None and forced < 1:
+            raise ValueError("num_splits must be >= 1")
+        sched, splits = get_mla_metadata(cache_seqlens, q.shape[1] * q.shape[2], 1,
+                                         forced_splits=forced)
+    return _decode(q, kv_cache, block_table, cache_seqlens, sched, splits, sm_scale, causal, out, lse)
+
+
+def merge_partials(part_o: torch.Tensor, part_lse: torch.Tensor, num_splits: torch.Tensor,
+                   dtype: torch.dtype = torch.bfloat16):
+    """LSE-weighted merge of explicit split partials (``mla_merge_partials``).
+
+    part_o ``[slots, rows, 512]`` fp32, part_lse ``[slots, rows]`` fp32 (log2 of each split's
+    softmax denominator), num_splits ``[B+1]`` int32 prefix sums -> ``(out [B, rows, 512],
+    lse [B, rows])`` with natural-log lse.
+    """
+    for t, n in ((part_o, "part_o"), (part_lse, "part_lse"), (num_splits, "num_splits")):
+        _require_gpu(t, n)
+    part_o = part_o.contiguous()
+    part_lse = part_lse.contiguous()
+    num_splits = num_splits.contiguous()
+    batch = num_splits.numel() - 1
+    rows = part_o.shape[1]
+    out = torch.empty(batch, rows, MLA_DIM_V, dtype=dtype, device=part_o.device)
+    lse = torch.empty(batch, rows, dtype=torch.float32, device=part_o.device)
+    check("mla_merge_partials", _lib.load().mla_merge_partials(
+        part_o.data_ptr(), part_lse.data_ptr(), num_splits.data_ptr(), batch, rows,
+        _DTYPES[dtype], out.data_ptr(), lse.data_ptr(), _stream_ptr(part_o.device)))
+    return out, lse
+
+
+def default_sm_scale() -> float:
+    return 1.0 / math.sqrt(MLA_DIM_QK)

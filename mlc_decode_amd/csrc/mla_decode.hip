@@ -1,0 +1,900 @@
+// mla_decode.hip -- MI355X (gfx950) split-KV MLA decode: main kernel, LSE combine,
+// tile-schedule kernel and the C ABI declared in include/mla_decode_amd.h.
+//
+// Math (the reference's fp32 oracle, test_mla.py:16-27, generalised to pages,
+// per-sequence lengths and causal s_q > 1):
+//   S = sm_scale * [q_nope|q_rope] . [kv_nope|kv_rope]^T   (576-d, one shared KV head)
+//   O = softmax(S) . kv_nope                                 (512-d, V = first 512 dims of K)
+//   lse = log(sum exp S)
+//
+// Kernel shape.  A workgroup owns one schedule part (a run of 64-token pages, possibly
+// spanning several sequences) for one block of R = NW*16*HT query rows, a row being a
+// (query token s, head h) pair.  Wave w owns rows [w*16*HT, (w+1)*16*HT) of the block.
+// The KV of a part is streamed in 32-token stages (36 KiB: 32 rows x 576 bf16) straight
+// from HBM into an LDS ring with global_load_lds_dwordx4 (no VGPR staging); each stage is
+// read once from HBM and shared by all waves of the workgroup.
+//
+// Per stage and wave, everything stays in the MFMA register layouts (16x16x32 bf16/f16):
+//   S^T[token, row] = K[token, :] . Q^T[:, row]      A = K from LDS (16-byte reads),
+//                                                    B = Q^T, resident in VGPRs
+//   P^T = exp2(S^T * sm_scale*log2e - m)             the S^T accumulator layout *is* the
+//                                                    B-operand layout of the next product
+//   O^T[dim, row] += V^T[dim, token] . P^T[token, row]
+//                                                    A = V^T via ds_read_b64_tr_b16 from
+//                                                    the same LDS stage (V is never
+//                                                    copied or re-read from HBM)
+// so the only cross-lane work is the row max / row sum over 4 lane groups.
+// Online softmax uses a lazily rescaled reference max: O and the row sums are rescaled
+// only when a row's stage max exceeds the reference by more than 2^8, which keeps every
+// P <= 256 (exact in fp32 sums, no bf16/f16 overflow) and skips almost all rescales.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+#include <mutex>
+#include <string>
+
+#include "mla_decode_amd.h"
+#include "mla_sched.h"
+
+namespace mla {
+
+constexpr int kDQK = 576;
+constexpr int kDV = 512;
+constexpr int kRopeOff = 512;
+constexpr int kStageTok = 32;
+constexpr int kRowChunks = kDQK / 8;                   // 72 16-byte chunks per token row
+constexpr int kRowBytes = kDQK * 2;                    // 1152
+constexpr int kStageBytes = kStageTok * kRowBytes;     // 36864
+constexpr int kLoadsPerStage = kStageBytes / 1024;     // 36 wave-wide 16-byte loads
+constexpr int kPanelBytes = kStageBytes / 2;           // 16 token rows
+constexpr int kKSteps = kDQK / 32;                     // 18 k-steps of the QK product
+constexpr int kDimTiles = kDV / 16;                    // 32 output dim tiles
+constexpr float kTau = 8.0f;                           // lazy-rescale threshold (log2 units)
+constexpr float kLn2 = 0.69314718055994530942f;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((__vector_size__(4 * sizeof(short))));
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef _Float16 f16x8 __attribute__((__vector_size__(8 * sizeof(_Float16))));
+#define LDS_AS __attribute__((address_space(3)))
+
+struct KParams {
+  const uint16_t* q_nope;
+  const uint16_t* q_rope;
+  int64_t q_sb, q_ss, q_sh;
+  int64_t qr_sb, qr_ss, qr_sh;
+  const uint16_t* kv_nope;
+  const uint16_t* kv_rope;
+  int64_t kv_sp, kv_st, kv_sb;
+  int64_t kr_sp, kr_st, kr_sb;
+  const int32_t* block_table;
+  int32_t bt_stride;
+  int32_t num_blocks;
+  const int32_t* seqlens;
+  const int32_t* sched;
+  const int32_t* splits;
+  uint16_t* out;
+  int64_t o_sb, o_ss, o_sh;
+  float* lse;
+  float* ws_lse;  // [slots, rows] log2-domain lse of each split
+  float* ws_o;    // [slots, rows, 512] softmax-normalised partial outputs
+  int32_t batch, s_q, heads, rows, causal, num_parts;
+  float scale_log2;  // sm_scale * log2(e)
+};
+
+// ---------------------------------------------------------------------------------------
+// small device helpers
+// ---------------------------------------------------------------------------------------
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma32(i32x4 a, i32x4 b, f32x4 c) {
+  if constexpr (DT == MLA_DTYPE_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (DT == MLA_DTYPE_BF16) {
+    const __bf16 x = (__bf16)a, y = (__bf16)b;  // round to nearest even
+    return (uint32_t)__builtin_bit_cast(uint16_t, x) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+  } else {
+    const _Float16 x = (_Float16)a, y = (_Float16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, x) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float to_f32(uint16_t v) {
+  if constexpr (DT == MLA_DTYPE_BF16) {
+    return __uint_as_float((uint32_t)v << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, v);
+  }
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// One wave-wide 16-byte-per-lane HBM -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes
+// land at LDS byte lds_addr + 16*l.  Issued as inline asm on purpose: the compiler then does
+// not track it as an LDS store, so it adds no conservative vmcnt(0) waits before the LDS
+// reads of *other* stages; completion is awaited explicitly (wait_stage) before a barrier.
+// M0 (the LDS base of the copy) is saved and restored around it.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+      : "memory");
+}
+
+// Workgroup barrier for LDS hand-off only.  Each wave has already waited for its own DMA
+// copies (vmcnt) and consumed its own LDS reads, so no memory-model fence is needed (the
+// fence __syncthreads() implies would wait for every in-flight stage load); the empty asm
+// statements keep the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ float wave_max_g(float v) {
+  // max over the 4 lane groups (lanes l, l^16, l^32, l^48) that hold one row
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_g(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// ---------------------------------------------------------------------------------------
+// stage loads: HBM -> LDS, 36 wave-wide 16-byte loads per 32-token stage
+// ---------------------------------------------------------------------------------------
+// LDS layout of a stage: two panels of 16 token rows; inside a panel the 16-byte chunk c
+// (dims 8c..8c+7) of row r sits at slot c*16 + (r ^ 8*(c&1)), i.e.
+//   byte(c, r) = ((r/16)*72*16 + c*16 + ((r%16) ^ ((c&1) << 3))) * 16.
+// Load i (one wave-wide global_load_lds_dwordx4 = 1 KiB) fills panel i/18, chunks
+// 4*(i%18) .. +3: lane l fetches chunk 4*(i%18) + l/16 of panel row (l%16) ^ 8*((l/16)&1),
+// so each lane's source is one per-stage base plus an immediate, and every token row
+// contributes 64 contiguous bytes per load.  Loads with i%18 >= 16 fetch the rope dims.
+template <int NW>
+__device__ __forceinline__ void issue_stage(uint8_t LDS_AS* slot, const uint16_t* nope_base,
+                                            const uint16_t* rope_base, int kv_st, int kr_st,
+                                            int last_row, int wave, int lane) {
+  const int prow = (lane & 15) ^ (((lane >> 4) & 1) << 3);
+  const int cl = (lane >> 4) * 8;  // element offset of the lane's chunk inside a load
+  const int r0 = prow < last_row ? prow : last_row;
+  const int r1 = prow + 16 < last_row ? prow + 16 : last_row;
+  // Rows past the sequence end re-read its last row: in bounds, finite, masked later.
+  const uint16_t* n0 = nope_base + (r0 * kv_st + cl);
+  const uint16_t* n1 = nope_base + (r1 * kv_st + cl);
+  const uint16_t* q0 = rope_base + (r0 * kr_st + cl);
+  const uint16_t* q1 = rope_base + (r1 * kr_st + cl);
+#pragma unroll
+  for (int j = 0; j < kLoadsPerStage / NW; ++j) {
+    const int i = wave + NW * j;  // NW divides 36, so i's panel and chunk are known per wave
+    const int panel = i >= 18;
+    const int ii = i - 18 * panel;
+    const uint16_t* src = ii < 16 ? (panel ? n1 : n0) + 32 * ii : (panel ? q1 : q0) + 32 * (ii - 16);
+    dma16(src, (uint32_t)(uintptr_t)(slot + i * 1024));
+  }
+}
+
+template <int NW, int NSTAGE>
+__device__ __forceinline__ void wait_stage(int after) {
+  // Wait until this wave's loads of the oldest outstanding stage have landed, with
+  // `after` younger stages allowed to stay in flight.
+  constexpr int per = kLoadsPerStage / NW;
+  if constexpr (NSTAGE >= 4) {
+    if (after >= 2) { wait_vmcnt<(2 * per < 64 ? 2 * per : 0)>(); return; }
+  }
+  if constexpr (NSTAGE >= 3) {
+    if (after >= 1) { wait_vmcnt<(per < 64 ? per : 0)>(); return; }
+  }
+  wait_vmcnt<0>();
+}
+
+__device__ __forceinline__ i32x4 lds_tr_pair(const uint8_t LDS_AS* p) {
+  // Two transposed 4x16 reads, one per 16-row panel: lane (g, i) gets V^T[i][4g..4g+3] and
+  // V^T[i][16+4g..16+4g+3] of the 16-column block its lane group addressed.
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 LDS_AS*)p);
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 LDS_AS*)(p + kPanelBytes));
+  const i32x2 lo2 = __builtin_bit_cast(i32x2, lo);
+  const i32x2 hi2 = __builtin_bit_cast(i32x2, hi);
+  return i32x4{lo2.x, lo2.y, hi2.x, hi2.y};
+}
+
+// ---------------------------------------------------------------------------------------
+// main split-KV kernel
+// ---------------------------------------------------------------------------------------
+template <int DT, int NW, int HT, int NSTAGE>
+__global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
+  static_assert((NSTAGE - 2) * (kLoadsPerStage / NW) < 64, "vmcnt would overflow");
+  static_assert(kLoadsPerStage % NW == 0, "loads per stage must split evenly");
+  constexpr int R = NW * 16 * HT;
+  constexpr int DK = 4;  // LDS prefetch depth of the QK A fragments
+  constexpr int DV = 4;  // LDS prefetch depth of the PV A fragments
+  __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[NSTAGE * kStageBytes];
+  uint8_t LDS_AS* smem = (uint8_t LDS_AS*)smem_raw;
+
+  const int part = blockIdx.x;
+  const int hb = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;   // lane group (MFMA k quarter / output row quarter)
+  const int li = lane & 15;  // lane within group
+  const int row0 = hb * R + wave * 16 * HT;
+
+  const int32_t* rec = p.sched + part * kSchedWords;
+  int b = rec[0];
+  int page = rec[1];
+  const int end_b = rec[2];
+  const int end_page = rec[3];
+  int split = rec[4];
+
+  // Per-lane LDS byte offsets that do not depend on the stage (panel layout above).
+  // QK A operand, fragment (kk, tt): token row 16*tt + li, chunk 4*kk + g.
+  const int k_lane = g * 256 + ((li ^ ((g & 1) << 3)) << 4);
+  // V^T A operand, dim tile dt: the lane addresses token row 4g + li/4 (and the same row of
+  // the second panel), bytes 32*dt + 8*(li%4), i.e. chunk 2*dt + (li%4)/2.
+  const int v_lane = ((li >> 1) & 1) * 256 + (((4 * g + (li >> 2)) ^ (((li >> 1) & 1) << 3)) << 4) +
+                     ((li & 1) << 3);
+
+  const int kv_st = (int)p.kv_st, kr_st = (int)p.kr_st;
+  const bool paged = p.block_table != nullptr;
+
+#pragma unroll 1
+  for (; b < p.batch; ++b, page = 0, split = 0) {
+    if (!(b < end_b || (b == end_b && page < end_page))) break;
+    const int L = p.seqlens[b] > 0 ? p.seqlens[b] : 0;
+    const int np = pages_of(L);
+    const int stop = (b == end_b) ? end_page : np;
+    const int st_begin = 2 * page;
+    const int st_end_seq = (L + kStageTok - 1) / kStageTok;
+    const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
+    const int nst = st_end > st_begin ? st_end - st_begin : 0;
+
+    // ---- query fragments (B operand of S^T = K Q^T), resident for the segment.  Rows
+    // past the end re-load the last row; their results are never written.
+    i32x4 qf[HT][kKSteps];
+    int lim[HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      int row = row0 + 16 * ht + li;
+      row = row < p.rows ? row : p.rows - 1;
+      const int s = row / p.heads;
+      const int h = row - s * p.heads;
+      lim[ht] = L - (p.causal ? (p.s_q - 1 - s) : 0);
+      const uint16_t* qn = p.q_nope + (b * p.q_sb + s * p.q_ss + h * p.q_sh) + 8 * g;
+      const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 8 * g;
+#pragma unroll
+      for (int kk = 0; kk < kKSteps; ++kk)
+        qf[ht][kk] = *(const i32x4*)(32 * kk < kRopeOff ? qn + 32 * kk : qr + (32 * kk - kRopeOff));
+    }
+    const int lmin = L - (p.causal ? p.s_q - 1 : 0);  // every row sees tokens < lmin
+
+    // ---- page-table cache: lane i holds the page id of page (pbase + i)
+    int pbase = page;
+    int bt_lane = 0;
+    if (paged) {
+      const int pi = pbase + lane;
+      int v = pi < np ? p.block_table[(int64_t)b * p.bt_stride + pi] : 0;
+      bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
+    }
+    wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
+
+    f32x4 o[kDimTiles][HT];
+#pragma unroll
+    for (int dt = 0; dt < kDimTiles; ++dt)
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) o[dt][ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_ref[HT], l_part[HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      m_ref[ht] = -INFINITY;
+      l_part[ht] = 0.f;
+    }
+
+#define MLA_ISSUE(KIDX)                                                                        \
+  do {                                                                                         \
+    const int st_ = st_begin + (KIDX);                                                         \
+    const uint16_t* nb_;                                                                       \
+    const uint16_t* rb_;                                                                       \
+    if (paged) {                                                                               \
+      const int pidx_ = st_ >> 1;                                                              \
+      if (pidx_ - pbase >= 64) {                                                               \
+        pbase = pidx_;                                                                         \
+        const int pi_ = pbase + lane;                                                          \
+        int v_ = pi_ < np ? p.block_table[(int64_t)b * p.bt_stride + pi_] : 0;                 \
+        bt_lane = v_ < 0 ? 0 : (v_ >= p.num_blocks ? p.num_blocks - 1 : v_);                   \
+      }                                                                                        \
+      const int pg_ = __builtin_amdgcn_readlane(bt_lane, pidx_ - pbase);                       \
+      const int tok_ = (st_ & 1) * kStageTok;                                                  \
+      nb_ = p.kv_nope + ((int64_t)pg_ * p.kv_sp + tok_ * kv_st);                               \
+      rb_ = p.kv_rope + ((int64_t)pg_ * p.kr_sp + tok_ * kr_st);                               \
+    } else {                                                                                   \
+      nb_ = p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st_ * kStageTok * kv_st);             \
+      rb_ = p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st_ * kStageTok * kr_st);             \
+    }                                                                                          \
+    const int left_ = L - st_ * kStageTok;                                                     \
+    issue_stage<NW>(smem + ((KIDX) % NSTAGE) * kStageBytes, nb_, rb_, kv_st, kr_st,            \
+                    (left_ < kStageTok ? left_ : kStageTok) - 1, wave, lane);                  \
+  } while (0)
+
+#pragma unroll
+    for (int k = 0; k < NSTAGE - 1; ++k)
+      if (k < nst) MLA_ISSUE(k);
+
+#pragma unroll 1
+    for (int k = 0; k < nst; ++k) {
+      const int remaining_after = nst - 1 - k;
+      wait_stage<NW, NSTAGE>(remaining_after < NSTAGE - 2 ? remaining_after : NSTAGE - 2);
+      lds_barrier();
+      if (k + NSTAGE - 1 < nst) MLA_ISSUE(k + NSTAGE - 1);
+
+      const uint8_t LDS_AS* sb = smem + (k % NSTAGE) * kStageBytes;
+      const int st = st_begin + k;
+
+      // ---- S^T = K Q^T over 576 dims: two 16-token tiles x HT 16-row tiles.
+      // Fragment n = 2*kk + tt; DK fragments in flight ahead of the MFMAs.
+      f32x4 acc[HT][2];
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) acc[ht][0] = acc[ht][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      i32x4 kf[DK];
+#define MLA_KFRAG(N) (*(const i32x4 LDS_AS*)(sb + k_lane + ((N) & 1) * kPanelBytes + ((N) >> 1) * 1024))
+#pragma unroll
+      for (int n = 0; n < DK; ++n) kf[n] = MLA_KFRAG(n);
+#pragma unroll
+      for (int n = 0; n < 2 * kKSteps; ++n) {
+        const i32x4 a = kf[n % DK];
+        if (n + DK < 2 * kKSteps) kf[n % DK] = MLA_KFRAG(n + DK);
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht)
+          acc[ht][n & 1] = mfma32<DT>(a, qf[ht][n >> 1], acc[ht][n & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#undef MLA_KFRAG
+
+      // ---- mask tokens past each row's limit (sequence tail / causal)
+      if (st * kStageTok + kStageTok > lmin) {
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = st * kStageTok + 16 * tt + 4 * g + r;
+              if (t >= lim[ht]) acc[ht][tt][r] = -INFINITY;
+            }
+      }
+
+      // ---- online softmax with a lazily moved reference max
+      float mx[HT];
+      bool need_any = false;
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        const float v = fmaxf(fmaxf(fmaxf(acc[ht][0][0], acc[ht][0][1]), fmaxf(acc[ht][0][2], acc[ht][0][3])),
+                              fmaxf(fmaxf(acc[ht][1][0], acc[ht][1][1]), fmaxf(acc[ht][1][2], acc[ht][1][3])));
+        mx[ht] = wave_max_g(v) * p.scale_log2;
+        need_any |= mx[ht] > m_ref[ht] + kTau;
+      }
+      if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          const bool need = mx[ht] > m_ref[ht] + kTau;
+          const float m_new = need ? mx[ht] : m_ref[ht];
+          const float alpha = need ? fast_exp2(m_ref[ht] - m_new) : 1.f;
+          m_ref[ht] = m_new;
+          l_part[ht] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < kDimTiles; ++dt) o[dt][ht] *= alpha;
+        }
+      }
+      i32x4 pb[HT];
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        const float mu = m_ref[ht] == -INFINITY ? 0.f : m_ref[ht];
+        float pv[2][4];
+        float sum = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
+            sum += pv[tt][r];
+          }
+        l_part[ht] += sum;
+        pb[ht] = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
+                       (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
+      }
+
+      // ---- O^T += V^T P^T over the 32 tokens of the stage; DV fragments in flight
+      i32x4 vf[DV];
+#define MLA_VFRAG(DTI) lds_tr_pair(sb + v_lane + (DTI) * 512)
+#pragma unroll
+      for (int n = 0; n < DV; ++n) vf[n] = MLA_VFRAG(n);
+#pragma unroll
+      for (int dt = 0; dt < kDimTiles; ++dt) {
+        const i32x4 a = vf[dt % DV];
+        if (dt + DV < kDimTiles) vf[dt % DV] = MLA_VFRAG(dt + DV);
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) o[dt][ht] = mfma32<DT>(a, pb[ht], o[dt][ht]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#undef MLA_VFRAG
+    }
+#undef MLA_ISSUE
+    lds_barrier();  // every wave is done with the LDS ring before it is refilled
+
+    // ---- epilogue: finish the row sums, normalise, write final or partial output
+    const int slot0 = p.splits[b];
+    const bool single = (p.splits[b + 1] - slot0) == 1;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      const float l = wave_sum_g(l_part[ht]);
+      const int row = row0 + 16 * ht + li;
+      if (row >= p.rows) continue;
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float lse2 = l > 0.f ? m_ref[ht] + __log2f(l) : -INFINITY;
+      const int s = row / p.heads;
+      const int h = row - s * p.heads;
+      if (single) {
+        uint16_t* dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          const f32x4 v = o[dt][ht] * inv;
+          *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
+        }
+        if (g == 0 && p.lse != nullptr)
+          p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
+      } else {
+        const int64_t slot = slot0 + split;
+        float* dst = p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < kDimTiles; ++dt) *(f32x4*)(dst + 16 * dt) = o[dt][ht] * inv;
+        if (g == 0) p.ws_lse[slot * p.rows + row] = lse2;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// combine: LSE-weighted merge of the splits of each (sequence, row)
+// ---------------------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restrict__ ws_o,
+                                                          const float* __restrict__ ws_lse,
+                                                          const int32_t* __restrict__ splits,
+                                                          int rows, int heads, int s_q,
+                                                          uint16_t* __restrict__ out,
+                                                          int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                                                          float* __restrict__ lse_out,
+                                                          int copy_single) {
+  __shared__ float w_sh[4][64];
+  const int b = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.y * 4 + wave;
+  if (row >= rows) return;
+  const int base = splits[b];
+  const int n = splits[b + 1] - base;
+  if (n < 1 || (n == 1 && !copy_single)) return;
+
+  float mx = -INFINITY;
+  for (int k = lane; k < n; k += 64) mx = fmaxf(mx, ws_lse[(int64_t)(base + k) * rows + row]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  float sum = 0.f;
+  if (mx != -INFINITY)
+    for (int k = lane; k < n; k += 64) sum += fast_exp2(ws_lse[(int64_t)(base + k) * rows + row] - mx);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const float lse2 = sum > 0.f ? mx + __log2f(sum) : -INFINITY;
+
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  for (int k0 = 0; k0 < n; k0 += 64) {
+    const int k = k0 + lane;
+    float w = 0.f;
+    if (k < n && lse2 != -INFINITY) w = fast_exp2(ws_lse[(int64_t)(base + k) * rows + row] - lse2);
+    w_sh[wave][lane] = w;
+    __builtin_amdgcn_wave_barrier();
+    const int kn = n - k0 < 64 ? n - k0 : 64;
+    for (int kk = 0; kk < kn; ++kk) {
+      const float wk = w_sh[wave][kk];
+      const float* src = ws_o + ((int64_t)(base + k0 + kk) * rows + row) * kDV + lane * 8;
+      const f32x4 x0 = *(const f32x4*)src;
+      const f32x4 x1 = *(const f32x4*)(src + 4);
+      acc[0] += wk * x0[0]; acc[1] += wk * x0[1]; acc[2] += wk * x0[2]; acc[3] += wk * x0[3];
+      acc[4] += wk * x1[0]; acc[5] += wk * x1[1]; acc[6] += wk * x1[2]; acc[7] += wk * x1[3];
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  const int s = row / heads;
+  const int h = row - s * heads;
+  uint16_t* dst = out + b * o_sb + s * o_ss + h * o_sh + lane * 8;
+  *(i32x4*)dst = i32x4{(int)pack2<DT>(acc[0], acc[1]), (int)pack2<DT>(acc[2], acc[3]),
+                       (int)pack2<DT>(acc[4], acc[5]), (int)pack2<DT>(acc[6], acc[7])};
+  if (lane == 0 && lse_out != nullptr) lse_out[((int64_t)b * heads + h) * s_q + s] = lse2 * kLn2;
+}
+
+// ---------------------------------------------------------------------------------------
+// tile schedule on the device: lengths staged in LDS, then one thread packs the parts
+// ---------------------------------------------------------------------------------------
+constexpr int kMetaMaxBatch = 16384;
+
+__global__ __launch_bounds__(256) void mla_metadata_kernel(const int32_t* __restrict__ seqlens,
+                                                           int batch, int num_parts,
+                                                           int fixed_overhead, int forced,
+                                                           int32_t* __restrict__ sched,
+                                                           int32_t* __restrict__ splits) {
+  __shared__ int32_t len_sh[kMetaMaxBatch];
+  for (int i = threadIdx.x; i < batch; i += blockDim.x) len_sh[i] = seqlens[i];
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  if (forced > 0)
+    schedule_forced(len_sh, batch, forced, sched, splits);
+  else
+    schedule_balanced(len_sh, batch, num_parts, fixed_overhead, sched, splits);
+}
+
+}  // namespace mla
+
+// =========================================================================================
+// C ABI
+// =========================================================================================
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+struct Variant {
+  int nw, ht, nstage;
+};
+
+// Rows per workgroup R = nw*16*ht; LDS per workgroup nstage*36 KiB.  Every variant keeps
+// one 16-row tile per wave (ht = 1): the query tile (72 VGPRs) and the fp32 output tile
+// (128 AGPRs) of a wave then fit the register file without spills.
+Variant pick_variant(int rows) {
+  if (rows <= 16) return {1, 1, 3};
+  if (rows <= 32) return {2, 1, 3};
+  return {4, 1, 4};
+}
+
+int wgs_per_cu(const Variant& v) {
+  const int lds = v.nstage * mla::kStageBytes;
+  int by_lds = (160 * 1024) / lds;
+  if (by_lds < 1) by_lds = 1;
+  const int by_waves = 4 / v.nw > 0 ? 4 / v.nw : 1;  // one wave per SIMD at full register use
+  return by_lds < by_waves ? by_lds : by_waves;
+}
+
+int cu_count_current() {
+  static std::once_flag once;
+  static int cached = 256;
+  std::call_once(once, [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cached = n;
+  });
+  return cached;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int64_t ws_lse_bytes(int64_t slots, int64_t rows) {
+  return ((slots * rows * 4) + 255) / 256 * 256;
+}
+
+template <int DT, int NW, int HT, int NS>
+hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) {
+  hipLaunchKernelGGL((mla::mla_splitkv_kernel<DT, NW, HT, NS>), dim3(kp.num_parts, head_blocks),
+                     dim3(NW * 64), 0, st, kp);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blocks, hipStream_t st) {
+  if (v.nw == 1) return launch_main<DT, 1, 1, 3>(kp, head_blocks, st);
+  if (v.nw == 2) return launch_main<DT, 2, 1, 3>(kp, head_blocks, st);
+  return launch_main<DT, 4, 1, 4>(kp, head_blocks, st);
+}
+
+int validate(const mla_decode_args* a, int64_t* need_ws) {
+  if (a == nullptr) return fail(MLA_ERR_INVALID, "args is NULL");
+  if (a->batch < 1 || a->s_q < 1 || a->heads_q < 1)
+    return fail(MLA_ERR_INVALID, "batch, s_q and heads_q must be >= 1");
+  if (a->heads_k != 1) return fail(MLA_ERR_UNSUPPORTED, "only heads_k == 1 (one latent KV head) is supported");
+  if (a->dtype != MLA_DTYPE_BF16 && a->dtype != MLA_DTYPE_F16)
+    return fail(MLA_ERR_INVALID, "dtype must be MLA_DTYPE_BF16 or MLA_DTYPE_F16");
+  if ((int64_t)a->s_q * a->heads_q > 65536) return fail(MLA_ERR_UNSUPPORTED, "s_q * heads_q exceeds 65536");
+  if (!(a->sm_scale > 0.f) || !isfinite(a->sm_scale)) return fail(MLA_ERR_INVALID, "sm_scale must be finite and > 0");
+  if (!a->q_nope || !a->q_rope || !a->kv_nope || !a->kv_rope || !a->out || !a->cache_seqlens ||
+      !a->tile_sched || !a->num_splits)
+    return fail(MLA_ERR_INVALID, "a required pointer is NULL");
+  if (!aligned(a->q_nope, 16) || !aligned(a->q_rope, 16) || !aligned(a->kv_nope, 16) ||
+      !aligned(a->kv_rope, 16))
+    return fail(MLA_ERR_INVALID, "q/kv pointers must be 16-byte aligned");
+  const int64_t s8[] = {a->q_stride_b, a->q_stride_s, a->q_stride_h, a->q_rope_stride_b,
+                        a->q_rope_stride_s, a->q_rope_stride_h, a->kv_stride_tok, a->kv_rope_stride_tok};
+  for (int64_t s : s8)
+    if (s < 0 || s % 8) return fail(MLA_ERR_INVALID, "q/kv strides must be non-negative multiples of 8 elements");
+  if (a->block_table) {
+    if (a->kv_stride_page < 0 || a->kv_stride_page % 8 || a->kv_rope_stride_page < 0 || a->kv_rope_stride_page % 8)
+      return fail(MLA_ERR_INVALID, "page strides must be non-negative multiples of 8 elements");
+    if (a->block_table_stride < 1) return fail(MLA_ERR_INVALID, "block_table_stride must be >= 1");
+    if (a->num_blocks < 1) return fail(MLA_ERR_INVALID, "num_blocks must be >= 1");
+  } else {
+    if (a->kv_stride_batch < 0 || a->kv_stride_batch % 8 || a->kv_rope_stride_batch < 0 ||
+        a->kv_rope_stride_batch % 8)
+      return fail(MLA_ERR_INVALID, "batch strides must be non-negative multiples of 8 elements");
+  }
+  if (!aligned(a->out, 8) || a->o_stride_b % 4 || a->o_stride_s % 4 || a->o_stride_h % 4 ||
+      a->o_stride_b < 0 || a->o_stride_s < 0 || a->o_stride_h < 0)
+    return fail(MLA_ERR_INVALID, "out must be 8-byte aligned with strides multiples of 4 elements");
+  if (a->num_parts < 1) return fail(MLA_ERR_INVALID, "num_parts must be >= 1");
+  *need_ws = mla_workspace_bytes(a->batch, a->s_q, a->heads_q, a->num_parts);
+  if (a->workspace == nullptr || a->workspace_bytes < *need_ws)
+    return fail(MLA_ERR_WORKSPACE, "workspace missing or smaller than mla_workspace_bytes()");
+  if (!aligned(a->workspace, 256)) return fail(MLA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return MLA_OK;
+}
+
+mla::KParams make_params(const mla_decode_args* a) {
+  mla::KParams k{};
+  k.q_nope = (const uint16_t*)a->q_nope;
+  k.q_rope = (const uint16_t*)a->q_rope;
+  k.q_sb = a->q_stride_b; k.q_ss = a->q_stride_s; k.q_sh = a->q_stride_h;
+  k.qr_sb = a->q_rope_stride_b; k.qr_ss = a->q_rope_stride_s; k.qr_sh = a->q_rope_stride_h;
+  k.kv_nope = (const uint16_t*)a->kv_nope;
+  k.kv_rope = (const uint16_t*)a->kv_rope;
+  k.kv_sp = a->kv_stride_page; k.kv_st = a->kv_stride_tok; k.kv_sb = a->kv_stride_batch;
+  k.kr_sp = a->kv_rope_stride_page; k.kr_st = a->kv_rope_stride_tok; k.kr_sb = a->kv_rope_stride_batch;
+  k.block_table = a->block_table;
+  k.bt_stride = a->block_table_stride;
+  k.num_blocks = a->num_blocks;
+  k.seqlens = a->cache_seqlens;
+  k.sched = a->tile_sched;
+  k.splits = a->num_splits;
+  k.out = (uint16_t*)a->out;
+  k.o_sb = a->o_stride_b; k.o_ss = a->o_stride_s; k.o_sh = a->o_stride_h;
+  k.lse = a->lse;
+  const int64_t rows = (int64_t)a->s_q * a->heads_q;
+  const int64_t slots = (int64_t)a->batch + a->num_parts;
+  k.ws_lse = (float*)a->workspace;
+  k.ws_o = (float*)((char*)a->workspace + ws_lse_bytes(slots, rows));
+  k.batch = a->batch;
+  k.s_q = a->s_q;
+  k.heads = a->heads_q;
+  k.rows = (int)rows;
+  k.causal = a->causal ? 1 : 0;
+  k.num_parts = a->num_parts;
+  k.scale_log2 = a->sm_scale * mla::kLog2e;
+  return k;
+}
+
+int launch_combine(const mla::KParams& k, int dtype, int copy_single, hipStream_t st) {
+  dim3 grid(k.batch, (k.rows + 3) / 4);
+  if (dtype == MLA_DTYPE_BF16)
+    hipLaunchKernelGGL(mla::mla_combine_kernel<MLA_DTYPE_BF16>, grid, dim3(256), 0, st, k.ws_o,
+                       k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
+                       k.lse, copy_single);
+  else
+    hipLaunchKernelGGL(mla::mla_combine_kernel<MLA_DTYPE_F16>, grid, dim3(256), 0, st, k.ws_o,
+                       k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
+                       k.lse, copy_single);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
+  return MLA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mla_version(void) { return MLA_DECODE_AMD_VERSION; }
+
+const char* mla_last_error(void) { return g_last_error.c_str(); }
+
+int mla_num_parts(int32_t batch, int32_t s_q, int32_t heads_q, int32_t heads_k, int32_t cu_count) {
+  if (batch < 1 || s_q < 1 || heads_q < 1 || heads_k != 1) {
+    fail(MLA_ERR_INVALID, "invalid shape");
+    return -MLA_ERR_INVALID;
+  }
+  const int rows = s_q * heads_q;
+  const Variant v = pick_variant(rows);
+  const int R = v.nw * 16 * v.ht;
+  const int head_blocks = (rows + R - 1) / R;
+  const int cus = cu_count > 0 ? cu_count : cu_count_current();
+  int parts = cus * wgs_per_cu(v) / head_blocks;
+  return parts < 1 ? 1 : parts;
+}
+
+int mla_get_metadata_host(const int32_t* cache_seqlens, int32_t batch, int32_t num_parts,
+                          int32_t fixed_overhead, int32_t forced_splits, int32_t* tile_sched,
+                          int32_t* num_splits) {
+  if (!cache_seqlens || !tile_sched || !num_splits) return fail(MLA_ERR_INVALID, "NULL pointer");
+  if (batch < 1) return fail(MLA_ERR_INVALID, "batch must be >= 1");
+  if (forced_splits > 0) {
+    if ((int64_t)num_parts != (int64_t)batch * forced_splits)
+      return fail(MLA_ERR_INVALID, "forced_splits requires num_parts == batch * forced_splits");
+    mla::schedule_forced(cache_seqlens, batch, forced_splits, tile_sched, num_splits);
+  } else {
+    if (num_parts < 1) return fail(MLA_ERR_INVALID, "num_parts must be >= 1");
+    mla::schedule_balanced(cache_seqlens, batch, num_parts,
+                           fixed_overhead < 0 ? mla::kDefaultFixedOverhead : fixed_overhead,
+                           tile_sched, num_splits);
+  }
+  return MLA_OK;
+}
+
+int mla_get_metadata(const int32_t* cache_seqlens, int32_t batch, int32_t num_parts,
+                     int32_t fixed_overhead, int32_t forced_splits, int32_t* tile_sched,
+                     int32_t* num_splits, void* stream) {
+  if (!cache_seqlens || !tile_sched || !num_splits) return fail(MLA_ERR_INVALID, "NULL pointer");
+  if (batch < 1 || batch > mla::kMetaMaxBatch) return fail(MLA_ERR_INVALID, "batch must be in [1, 16384]");
+  if (forced_splits > 0) {
+    if ((int64_t)num_parts != (int64_t)batch * forced_splits)
+      return fail(MLA_ERR_INVALID, "forced_splits requires num_parts == batch * forced_splits");
+  } else if (num_parts < 1) {
+    return fail(MLA_ERR_INVALID, "num_parts must be >= 1");
+  }
+  hipLaunchKernelGGL(mla::mla_metadata_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream,
+                     cache_seqlens, batch, num_parts,
+                     fixed_overhead < 0 ? mla::kDefaultFixedOverhead : fixed_overhead,
+                     forced_splits, tile_sched, num_splits);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("metadata launch failed: ") + hipGetErrorString(e));
+  return MLA_OK;
+}
+
+int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t num_parts) {
+  if (batch < 1 || s_q < 1 || heads_q < 1 || num_parts < 1) return 0;
+  const int64_t rows = (int64_t)s_q * heads_q;
+  const int64_t slots = (int64_t)batch + num_parts;
+  return ws_lse_bytes(slots, rows) + slots * rows * mla::kDV * 4;
+}
+
+int mla_decode_fwd(const mla_decode_args* args, void* stream) {
+  int64_t need = 0;
+  const int rc = validate(args, &need);
+  if (rc != MLA_OK) return rc;
+  const mla::KParams kp = make_params(args);
+  const Variant v = pick_variant(kp.rows);
+  const int R = v.nw * 16 * v.ht;
+  const int head_blocks = (kp.rows + R - 1) / R;
+  hipStream_t st = (hipStream_t)stream;
+  const hipError_t e = args->dtype == MLA_DTYPE_BF16
+                           ? launch_main_dt<MLA_DTYPE_BF16>(v, kp, head_blocks, st)
+                           : launch_main_dt<MLA_DTYPE_F16>(v, kp, head_blocks, st);
+  if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("decode launch failed: ") + hipGetErrorString(e));
+  return launch_combine(kp, args->dtype, 0, st);
+}
+
+int mla_combine_fwd(const mla_decode_args* args, void* stream) {
+  int64_t need = 0;
+  const int rc = validate(args, &need);
+  if (rc != MLA_OK) return rc;
+  return launch_combine(make_params(args), args->dtype, 0, (hipStream_t)stream);
+}
+
+int mla_merge_partials(const float* part_o, const float* part_lse, const int32_t* num_splits,
+                       int32_t batch, int32_t rows, int32_t dtype, void* out, float* lse_out,
+                       void* stream) {
+  if (!part_o || !part_lse || !num_splits || !out) return fail(MLA_ERR_INVALID, "NULL pointer");
+  if (batch < 1 || rows < 1) return fail(MLA_ERR_INVALID, "batch and rows must be >= 1");
+  if (dtype != MLA_DTYPE_BF16 && dtype != MLA_DTYPE_F16) return fail(MLA_ERR_INVALID, "bad dtype");
+  if (!aligned(part_o, 16) || !aligned(out, 16)) return fail(MLA_ERR_INVALID, "part_o and out must be 16-byte aligned");
+  mla::KParams k{};
+  k.ws_o = (float*)part_o;
+  k.ws_lse = (float*)part_lse;
+  k.splits = num_splits;
+  k.batch = batch;
+  k.rows = rows;
+  k.heads = rows;
+  k.s_q = 1;
+  k.out = (uint16_t*)out;
+  k.o_sb = (int64_t)rows * mla::kDV;
+  k.o_ss = 0;
+  k.o_sh = mla::kDV;
+  k.lse = lse_out;
+  return launch_combine(k, dtype, 1, (hipStream_t)stream);
+}
+
+int mla_split_plan(int32_t seqlen_kv, int32_t num_split, int32_t block_n, int32_t spread,
+                   int32_t* ns_out, int32_t* blocks_per_split_out, int32_t* extra_out) {
+  if (seqlen_kv < 1 || num_split < 1 || block_n < 1 || !ns_out || !blocks_per_split_out || !extra_out)
+    return fail(MLA_ERR_INVALID, "seqlen_kv, num_split and block_n must be >= 1");
+  const int nb = (seqlen_kv + block_n - 1) / block_n;
+  if (!spread) {
+    const int chunk = (seqlen_kv + num_split - 1) / num_split;
+    int bpc = (chunk + block_n - 1) / block_n;
+    if (bpc < 1) bpc = 1;
+    int ns = (nb + bpc - 1) / bpc;
+    if (ns < 1) ns = 1;
+    *ns_out = ns;
+    *blocks_per_split_out = bpc;
+    *extra_out = 0;
+  } else {
+    int ns = num_split < nb ? num_split : nb;
+    if (ns < 1) ns = 1;
+    *ns_out = ns;
+    *blocks_per_split_out = nb / ns;
+    *extra_out = nb % ns;
+  }
+  return MLA_OK;
+}
+
+int mla_launch(const void* q, const void* q_pe, const void* kv, const void* k_pe, void* out,
+               int32_t batch, int32_t heads, int32_t kv_ctx, int32_t dtype,
+               const int32_t* cache_seqlens, const int32_t* tile_sched, int32_t num_parts,
+               const int32_t* num_splits, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (kv_ctx < 1) return fail(MLA_ERR_INVALID, "kv_ctx must be >= 1");
+  mla_decode_args a{};
+  a.batch = batch;
+  a.s_q = 1;
+  a.heads_q = heads;
+  a.heads_k = 1;
+  a.dtype = dtype;
+  a.causal = 0;
+  a.sm_scale = 1.0f / sqrtf((float)MLA_DIM_QK);
+  a.num_blocks = 1;
+  a.q_nope = q;
+  a.q_rope = q_pe;
+  a.q_stride_b = (int64_t)heads * 512;
+  a.q_stride_s = 0;
+  a.q_stride_h = 512;
+  a.q_rope_stride_b = (int64_t)heads * 64;
+  a.q_rope_stride_s = 0;
+  a.q_rope_stride_h = 64;
+  a.kv_nope = kv;
+  a.kv_rope = k_pe;
+  a.kv_stride_tok = 512;
+  a.kv_stride_batch = (int64_t)kv_ctx * 512;
+  a.kv_rope_stride_tok = 64;
+  a.kv_rope_stride_batch = (int64_t)kv_ctx * 64;
+  a.block_table = nullptr;
+  a.num_parts = num_parts;
+  a.cache_seqlens = cache_seqlens;
+  a.tile_sched = tile_sched;
+  a.num_splits = num_splits;
+  a.out = out;
+  a.o_stride_b = (int64_t)heads * 512;
+  a.o_stride_s = 0;
+  a.o_stride_h = 512;
+  a.lse = nullptr;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  return mla_decode_fwd(&a, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,156 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the header
+declares, its host-side schedule and split rule agree with the oracle, and bad arguments
+come back as nonzero statuses with messages (validation runs before any HIP call)."""
+import ctypes
+import os
+import random
+import re
+
+import pytest
+import torch
+
+from mlc_decode_amd import _lib
+from mlc_decode_amd._lib import MlaDecodeArgs
+from mlc_decode_amd.api import get_mla_metadata_host
+from oracle import mla_ref as R
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "mla_decode_amd.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z0-9_]+\*?\s+\**(mla_[a-z0-9_]+)\(", text, re.M)))
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = header_functions()
+    assert len(declared) >= 10
+    assert sorted(_lib.EXPORTED) == declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.mla_version() == 1
+    assert lib.mla_last_error() is not None
+
+
+def test_struct_layout_matches_header():
+    # 8 int/float fields, then pointers / int64s; spot-check offsets the C side relies on
+    assert MlaDecodeArgs.q_nope.offset == 32
+    assert ctypes.sizeof(MlaDecodeArgs) % 8 == 0
+    assert MlaDecodeArgs.workspace_bytes.offset == ctypes.sizeof(MlaDecodeArgs) - 8
+
+
+def test_split_plan_matches_reference_rule(lib):
+    ns, bpc, ex = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    for L in (1, 7, 33, 64, 65, 2048, 3000, 4095, 8192, 65536):
+        for req in (1, 3, 64, 104, 312):
+            for bn in (32, 64):
+                for spread in (0, 1):
+                    assert lib.mla_split_plan(L, req, bn, spread, ctypes.byref(ns), ctypes.byref(bpc),
+                                              ctypes.byref(ex)) == 0
+                    assert (ns.value, bpc.value, ex.value) == R.split_plan(L, req, bn, bool(spread))
+    assert lib.mla_split_plan(0, 4, 32, 0, ctypes.byref(ns), ctypes.byref(bpc), ctypes.byref(ex)) != 0
+    assert b"seqlen_kv" in lib.mla_last_error()
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_host_schedule_matches_oracle(seed):
+    rng = random.Random(100 + seed)
+    B = rng.choice([1, 2, 64, 128, 132])
+    lengths = [rng.choice([0, 1, 64, 65, rng.randint(1, 16384)]) for _ in range(B)]
+    for parts in (1, 5, 128, 256):
+        for fo in (0, 5):
+            sched, splits = get_mla_metadata_host(lengths, parts, fo)
+            recs, prefix = R.schedule_balanced(lengths, parts, fo)
+            assert sched[:, :5].tolist() == [list(r) for r in recs]
+            assert torch.all(sched[:, 5:] == 0)
+            assert splits.tolist() == prefix
+    for forced in (1, 3, 8):
+        sched, splits = get_mla_metadata_host(lengths, 0, forced_splits=forced)
+        recs, prefix = R.schedule_forced(lengths, forced)
+        assert sched[:, :5].tolist() == [list(r) for r in recs]
+        assert splits.tolist() == prefix
+
+
+def test_workspace_bytes(lib):
+    n = lib.mla_workspace_bytes(64, 1, 128, 128)
+    slots, rows = 64 + 128, 128
+    assert n == -(-slots * rows * 4 // 256) * 256 + slots * rows * 512 * 4
+    assert lib.mla_workspace_bytes(0, 1, 16, 4) == 0
+
+
+def test_num_parts(lib):
+    # 16 / 32 / 64 rows -> one workgroup per CU; 128 rows -> two head blocks share a CU count
+    assert lib.mla_num_parts(1, 1, 16, 1, 256) == 256
+    assert lib.mla_num_parts(64, 1, 128, 1, 256) == 128
+    assert lib.mla_num_parts(32, 2, 128, 1, 256) == 64
+    assert lib.mla_num_parts(1, 1, 16, 2, 256) < 0
+
+
+def _valid_args():
+    a = MlaDecodeArgs()
+    a.batch, a.s_q, a.heads_q, a.heads_k = 2, 1, 16, 1
+    a.dtype, a.causal, a.sm_scale, a.num_blocks = 0, 1, 576 ** -0.5, 4
+    base = 1 << 20  # fake, aligned device addresses: validation fails before any use
+    a.q_nope, a.q_rope = base, base + 1024
+    a.q_stride_b = a.q_rope_stride_b = 16 * 576
+    a.q_stride_h = a.q_rope_stride_h = 576
+    a.kv_nope, a.kv_rope = base, base + 1024
+    a.kv_stride_page = a.kv_rope_stride_page = 64 * 576
+    a.kv_stride_tok = a.kv_rope_stride_tok = 576
+    a.block_table, a.block_table_stride = base, 2
+    a.num_parts = 4
+    a.cache_seqlens = a.tile_sched = a.num_splits = base
+    a.out = base
+    a.o_stride_b, a.o_stride_h = 16 * 512, 512
+    a.workspace = base
+    a.workspace_bytes = 0
+    return a
+
+
+@pytest.mark.parametrize("field,value,code,needle", [
+    ("heads_k", 2, 4, b"heads_k"),
+    ("dtype", 7, 1, b"dtype"),
+    ("batch", 0, 1, b"batch"),
+    ("kv_nope", (1 << 20) + 8, 1, b"16-byte"),
+    ("kv_stride_tok", 577, 1, b"strides"),
+    ("num_parts", 0, 1, b"num_parts"),
+    ("sm_scale", 0.0, 1, b"sm_scale"),
+    ("workspace_bytes", 0, 2, b"workspace"),
+])
+def test_decode_rejects_bad_args(lib, field, value, code, needle):
+    a = _valid_args()
+    setattr(a, field, value)
+    rc = lib.mla_decode_fwd(ctypes.byref(a), None)
+    assert rc == code
+    assert needle in lib.mla_last_error()
+    with pytest.raises(_lib.MlaError):
+        _lib.check("mla_decode_fwd", rc)
+
+
+def test_metadata_rejects_bad_args(lib):
+    seq = (ctypes.c_int32 * 2)(5, 6)
+    sched = (ctypes.c_int32 * 64)()
+    splits = (ctypes.c_int32 * 3)()
+    assert lib.mla_get_metadata_host(seq, 2, 3, -1, 2, sched, splits) != 0   # parts != B*forced
+    assert b"forced_splits" in lib.mla_last_error()
+    assert lib.mla_get_metadata_host(seq, 0, 3, -1, 0, sched, splits) != 0
+    assert lib.mla_get_metadata(None, 2, 3, -1, 0, None, None, None) != 0
+
+
+def test_python_api_refuses_cpu_tensors():
+    from mlc_decode_amd import MlaKernel, mla_decode_with_kvcache
+    k = MlaKernel(1, 16, 1, 64)
+    x = torch.zeros(1, 16, 512, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        k(x, torch.zeros(1, 16, 64, dtype=torch.float16), torch.zeros(1, 64, 1, 512, dtype=torch.float16),
+          torch.zeros(1, 64, 1, 64, dtype=torch.float16))
+    with pytest.raises(ValueError):
+        mla_decode_with_kvcache(torch.zeros(1, 1, 16, 576), torch.zeros(1, 64, 1, 576),
+                                torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        MlaKernel(1, 16, 2, 64)

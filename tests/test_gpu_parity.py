@@ -1,0 +1,260 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on identical inputs.
+
+Bar: output max-abs error <= 1e-2 and cosine >= 0.99999 against the
+fp32 oracle, LSE within 1e-3; rows with no visible key must give out == 0, lse == -inf.
+Full-size benchmark configs are checked on a sample of their sequences (oracle cost) plus
+whole-output properties.
+"""
+import math
+import sys
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mlc_decode_amd import (MlaKernel, flash_mla_with_kvcache, get_mla_metadata,
+                            get_mla_metadata_host, merge_partials, mla_decode_with_kvcache)
+from mlc_decode_amd.inputs import CONFIGS, MlaConfig, make_inputs
+from oracle import mla_ref as R
+
+pytestmark = pytest.mark.gpu
+
+OUT_ATOL = 1e-2
+COS_MIN = 0.99999
+LSE_ATOL = 1e-3
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def assert_parity(out, lse, ref_out, ref_lse, what=""):
+    o = out.float().cpu()
+    r = ref_out.float()
+    assert torch.isfinite(o).all(), f"{what}: non-finite output"
+    err = (o - r).abs().max().item()
+    assert err <= OUT_ATOL, f"{what}: max-abs {err}"
+    if r.abs().max() > 0:
+        cos = F.cosine_similarity(o.flatten().double(), r.flatten().double(), dim=0).item()
+        assert cos >= COS_MIN, f"{what}: cosine {cos}"
+    if lse is not None:
+        lg = lse.float().cpu()
+        fin = torch.isfinite(ref_lse)
+        assert torch.equal(torch.isfinite(lg), fin), f"{what}: lse finiteness differs"
+        assert torch.all(lg[~fin] == -math.inf), f"{what}: empty rows must have lse = -inf"
+        if fin.any():
+            lerr = (lg[fin] - ref_lse[fin]).abs().max().item()
+            assert lerr <= LSE_ATOL, f"{what}: lse err {lerr}"
+
+
+def run_paged(inp, device, num_splits=None):
+    d = inp.to(device)
+    out, lse = mla_decode_with_kvcache(d.q, d.kv_cache, d.block_table, d.cache_seqlens,
+                                       num_splits=num_splits, sm_scale=inp.sm_scale, causal=inp.causal)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def oracle_rows(inp, rows):
+    """Oracle on a subset of sequences (indices `rows`)."""
+    idx = torch.tensor(rows)
+    return R.decode_paged(inp.q[idx], inp.kv_cache, inp.block_table[idx], inp.cache_seqlens[idx],
+                          inp.sm_scale, inp.causal)
+
+
+def small_cfg(name, B, s_q, H, lengths, dtype=torch.bfloat16, sigma=1.0, causal=True):
+    return MlaConfig(name, batch=B, s_q=s_q, heads=H, dtype=dtype, sigma=sigma, causal=causal,
+                     seqlen_groups=[(1, L) for L in lengths])
+
+
+# ---------------------------------------------------------------- small exhaustive cases
+TAILS = [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 1000]
+
+
+@pytest.mark.parametrize("H", [16, 32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_tails_all_head_counts(gpu, H, dtype):
+    cfg = small_cfg(f"tails_h{H}", len(TAILS), 1, H, TAILS, dtype)
+    inp = make_inputs(cfg, seed=H)
+    for ns in (None, 1, 3):
+        say(f"tails H={H} dtype={dtype} num_splits={ns}")
+        out, lse = run_paged(inp, gpu, ns)
+        ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                      inp.sm_scale, inp.causal)
+        assert_parity(out, lse, ref_o, ref_l, f"H={H} ns={ns}")
+
+
+@pytest.mark.parametrize("H", [16, 64, 128])
+def test_causal_two_queries(gpu, H):
+    lengths = [1, 2, 33, 64, 65, 300]
+    cfg = small_cfg(f"sq2_h{H}", len(lengths), 2, H, lengths)
+    inp = make_inputs(cfg, seed=7)
+    for ns in (None, 2):
+        say(f"causal s_q=2 H={H} num_splits={ns}")
+        out, lse = run_paged(inp, gpu, ns)
+        ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                      inp.sm_scale, True)
+        assert_parity(out, lse, ref_o, ref_l, f"sq2 H={H} ns={ns}")
+    # L = 1: query 0 sees no key
+    assert torch.all(out[0, 0].float() == 0)
+
+
+def test_non_causal_two_queries(gpu):
+    cfg = small_cfg("sq2_nc", 3, 2, 16, [5, 64, 200], causal=False)
+    inp = make_inputs(cfg, seed=8)
+    say("non-causal s_q=2")
+    out, lse = run_paged(inp, gpu)
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                  inp.sm_scale, False)
+    assert_parity(out, lse, ref_o, ref_l, "non-causal")
+
+
+def test_empty_sequence_and_nan_padding(gpu):
+    lengths = [0, 37, 1, 64, 130]
+    cfg = small_cfg("edge", len(lengths), 1, 16, lengths)
+    inp = make_inputs(cfg, seed=9)
+    # poison every cache row past each sequence end, and unused table slots
+    for b, L in enumerate(lengths):
+        n = R.pages_of(L)
+        if n and L % 64:
+            inp.kv_cache[inp.block_table[b, n - 1].long(), L % 64:] = float("nan")
+        inp.block_table[b, n:] = 1 << 30
+    say("empty sequence + NaN padding")
+    out, lse = run_paged(inp, gpu, 1)
+    good = torch.tensor(lengths) > 0
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                  inp.sm_scale, True)
+    assert_parity(out, lse, ref_o, ref_l, "edge")
+    assert torch.all(out[~good].float() == 0) and torch.all(lse[~good].cpu() == -math.inf)
+
+
+def test_golden_fixtures_on_gpu(gpu):
+    import numpy as np
+    from test_oracle import GOLDEN, load_case
+    z = np.load(GOLDEN)
+    for name in sorted({k.split(".")[0] for k in z.files}):
+        c = load_case(z, name)
+        say(f"golden {name}")
+        d = lambda t: t.to(gpu)  # noqa: E731
+        out, lse = mla_decode_with_kvcache(d(c["q"]), d(c["kv"]), d(c["table"]), d(c["lengths"]),
+                                           sm_scale=R.D_QK ** -0.5, causal=c["causal"])
+        torch.cuda.synchronize()
+        assert_parity(out, lse, c["out"], c["lse"], name)
+
+
+def test_schedule_device_matches_host(gpu):
+    lengths = [0, 1, 4096, 65, 16384, 128, 7000]
+    seq = torch.tensor(lengths, dtype=torch.int32, device=gpu)
+    for parts, fo, forced in ((256, -1, 0), (7, 0, 0), (0, -1, 3)):
+        say(f"schedule parts={parts} fo={fo} forced={forced}")
+        s_d, n_d = get_mla_metadata(seq, 16, 1, num_parts=parts or None, fixed_overhead=fo,
+                                    forced_splits=forced)
+        s_h, n_h = get_mla_metadata_host(lengths, parts, fo, forced)
+        torch.cuda.synchronize()
+        assert torch.equal(s_d.cpu(), s_h) and torch.equal(n_d.cpu(), n_h)
+
+
+def test_flash_mla_call_shape(gpu):
+    cfg = small_cfg("flash", 2, 1, 16, [100, 2000])
+    inp = make_inputs(cfg, seed=11).to(gpu)
+    say("flash_mla_with_kvcache")
+    meta, splits = get_mla_metadata(inp.cache_seqlens, 16, 1)
+    out, lse = flash_mla_with_kvcache(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, 512,
+                                      meta, splits, causal=True)
+    cpu = make_inputs(cfg, seed=11)
+    ref_o, ref_l = R.decode_paged(cpu.q, cpu.kv_cache, cpu.block_table, cpu.cache_seqlens,
+                                  cpu.sm_scale, True)
+    assert_parity(out, lse, ref_o, ref_l, "flash_mla")
+
+
+def test_split_latent_rope_views(gpu):
+    cfg = small_cfg("views", 2, 1, 16, [70, 130])
+    cpu = make_inputs(cfg, seed=12)
+    inp = cpu.to(gpu)
+    latent = inp.kv_cache[..., :512].contiguous()
+    rope = inp.kv_cache[..., 512:].contiguous()
+    say("separate latent / rope tensors")
+    out, lse = mla_decode_with_kvcache(inp.q, (latent, rope), inp.block_table, inp.cache_seqlens)
+    ref_o, ref_l = R.decode_paged(cpu.q, cpu.kv_cache, cpu.block_table, cpu.cache_seqlens,
+                                  cpu.sm_scale, True)
+    assert_parity(out, lse, ref_o, ref_l, "views")
+
+
+def test_merge_partials(gpu):
+    g = torch.Generator().manual_seed(13)
+    splits = torch.tensor([0, 3, 4, 9], dtype=torch.int32)
+    rows = 20
+    part_o = torch.randn(9, rows, 512, generator=g)
+    part_l2 = torch.randn(9, rows, generator=g) * 4
+    part_l2[1, 3] = -math.inf           # one empty split
+    part_l2[3, :] = -math.inf           # a sequence whose only split is empty
+    say("merge_partials")
+    out, lse = merge_partials(part_o.to(gpu), part_l2.to(gpu), splits.to(gpu), torch.bfloat16)
+    torch.cuda.synchronize()
+    ln = part_l2 * math.log(2)
+    for b in range(3):
+        a, e = int(splits[b]), int(splits[b + 1])
+        ro, rl = R.combine(part_o[a:e], ln[a:e])
+        if e - a == 1 and torch.isinf(rl).all():
+            ro = part_o[a] * 0
+        assert_parity(out[b].unsqueeze(0), lse[b].unsqueeze(0), ro.unsqueeze(0), rl.unsqueeze(0),
+                      f"merge b={b}")
+
+
+# ---------------------------------------------------------------- reference call shapes
+@pytest.mark.parametrize("kv_ctx", [7, 33, 2048, 3000, 3008, 4095, 4096])
+def test_reference_contiguous_layout(gpu, kv_ctx, monkeypatch):
+    import baseline_mla
+    import mla_decode
+    monkeypatch.setattr(mla_decode, "_AUTOTUNE_ENABLED", False)
+    g = torch.Generator().manual_seed(kv_ctx)
+    b, h = 1, 16
+    mk = lambda *s: (torch.randn(*s, generator=g) * 0.1).to(torch.float16)  # noqa: E731
+    q, q_pe, kv, k_pe = mk(b, h, 512), mk(b, h, 64), mk(b, kv_ctx, 1, 512), mk(b, kv_ctx, 1, 64)
+    ref = R.decode_contiguous(q, q_pe, kv, k_pe)
+    args = [t.to(gpu) for t in (q, q_pe, kv, k_pe)]
+    for name, kern in (("mla_decode", mla_decode._get_kernel(b, h, 1, kv_ctx, 512, 64)),
+                       ("baseline_mla", baseline_mla._get_kernel(b, h, 1, kv_ctx, 512, 64)),
+                       ("explicit ns=5", mla_decode.build_kernel_from_config(
+                           b, h, 1, kv_ctx, 512, 64, {"num_split": 5, "block_N": 32, "block_H": 16}))):
+        say(f"contiguous {name} kv_ctx={kv_ctx}")
+        out = torch.empty_like(args[0])
+        kern(*args, out)
+        torch.cuda.synchronize()
+        assert_parity(out, None, ref, None, f"{name} ctx={kv_ctx}")
+    assert_parity(baseline_mla.ref_program(*args), None, ref, None, "ref_program")
+
+
+def test_reference_autotune_path(gpu):
+    import mla_decode
+    say("mla_decode._get_kernel autotune b=2 h=64 ctx=1500")
+    k = mla_decode._get_kernel(2, 64, 1, 1500, 512, 64)
+    g = torch.Generator().manual_seed(3)
+    mk = lambda *s: (torch.randn(*s, generator=g) * 0.1).to(torch.float16)  # noqa: E731
+    q, q_pe, kv, k_pe = mk(2, 64, 512), mk(2, 64, 64), mk(2, 1500, 1, 512), mk(2, 1500, 1, 64)
+    out = k(*[t.to(gpu) for t in (q, q_pe, kv, k_pe)])
+    torch.cuda.synchronize()
+    assert_parity(out, None, R.decode_contiguous(q, q_pe, kv, k_pe), None, "autotuned")
+
+
+# ---------------------------------------------------------------- benchmark configs
+SAMPLES = {"C1": [0], "C2": [0, 17, 63], "C3": None, "C4": [0, 31], "C5": None}
+
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+def test_benchmark_config(gpu, name):
+    cfg = CONFIGS[name]
+    inp = make_inputs(cfg, seed=0)
+    L = inp.cache_seqlens
+    rows = SAMPLES[name]
+    if rows is None:  # ragged: the longest, the shortest and a few in between
+        order = torch.argsort(L).tolist()
+        rows = sorted({order[0], order[1], order[len(order) // 2], order[-2], order[-1]})
+    say(f"config {name} B={cfg.batch} H={cfg.heads} s_q={cfg.s_q} sampled rows {rows}")
+    out, lse = run_paged(inp, gpu, cfg.num_splits)
+    assert torch.isfinite(out.float()).all()
+    assert torch.isfinite(lse).all() or cfg.s_q > 1
+    ref_o, ref_l = oracle_rows(inp, rows)
+    idx = torch.tensor(rows)
+    assert_parity(out.cpu()[idx], lse.cpu()[idx], ref_o, ref_l, name)

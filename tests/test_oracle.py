@@ -1,0 +1,221 @@
+"""Pins the CPU oracle (oracle/mla_ref.py) before it is trusted as the GPU checker.
+
+Each check is one a plausible oracle mistake fails: a library routine computed
+independently (torch SDPA / logsumexp in float64, via the committed fixtures), closed
+forms (L = 1, q = 0, identical keys), invariances (page permutation, splitting + merge,
+query scaling), the causal rule (s_q = 2 rows vs s_q = 1 decodes) and brute-force integer
+checks of the split rule and the schedules.
+"""
+import math
+import os
+import random
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import mla_ref as R
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "mla_cases.npz")
+
+
+def load_case(z, name):
+    s_q, H, dt, causal = (int(x) for x in z[f"{name}.meta"])
+    dtype = torch.bfloat16 if dt == 0 else torch.float16
+    q = torch.from_numpy(z[f"{name}.q"]).view(dtype)
+    kv = torch.from_numpy(z[f"{name}.kv"]).view(dtype)
+    return dict(q=q, kv=kv, table=torch.from_numpy(z[f"{name}.table"]),
+                lengths=torch.from_numpy(z[f"{name}.lengths"]), causal=bool(causal),
+                out=torch.from_numpy(z[f"{name}.out"]), lse=torch.from_numpy(z[f"{name}.lse"]))
+
+
+def rand_paged(B, s_q, H, lengths, dtype=torch.float32, seed=0, sigma=1.0):
+    g = torch.Generator().manual_seed(seed)
+    pages = [R.pages_of(L) for L in lengths]
+    total = max(sum(pages), 1)
+    perm = torch.randperm(total, generator=g)
+    table = torch.zeros(B, max(max(pages), 1), dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(pages):
+        table[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    q = (torch.randn(B, s_q, H, R.D_QK, generator=g) * sigma).to(dtype)
+    kv = (torch.randn(total, R.PAGE, 1, R.D_QK, generator=g) * sigma).to(dtype)
+    return q, kv, table, torch.tensor(lengths, dtype=torch.int32)
+
+
+SCALE = R.D_QK ** -0.5
+
+
+def test_golden_fixtures():
+    z = np.load(GOLDEN)
+    names = sorted({k.split(".")[0] for k in z.files})
+    assert len(names) >= 6
+    for name in names:
+        c = load_case(z, name)
+        out, lse = R.decode_paged(c["q"], c["kv"], c["table"], c["lengths"], SCALE, c["causal"])
+        assert torch.allclose(out, c["out"], atol=2e-5, rtol=1e-4), name
+        fin = torch.isfinite(c["lse"])
+        assert torch.equal(fin, torch.isfinite(lse)), name
+        assert torch.allclose(lse[fin], c["lse"][fin], atol=2e-5, rtol=1e-5), name
+        assert torch.all(out[~fin.permute(0, 2, 1)] == 0), name
+
+
+def test_sdpa_library_float64():
+    q, kv, table, lens = rand_paged(3, 1, 16, [1, 70, 190], torch.float64, seed=3)
+    out, _ = R.decode_paged(q, kv, table, lens, SCALE, causal=True, dtype=torch.float64)
+    for b in range(3):
+        k = R.gather(kv[:, :, 0], table[b], int(lens[b]))
+        ref = F.scaled_dot_product_attention(q[b].transpose(0, 1).unsqueeze(0),
+                                             k.expand(16, -1, -1).unsqueeze(0),
+                                             k[:, :512].expand(16, -1, -1).unsqueeze(0), scale=SCALE)
+        assert torch.allclose(out[b, 0], ref[0, :, 0], atol=1e-12)
+
+
+def test_length_one_closed_form():
+    q, kv, table, lens = rand_paged(2, 1, 16, [1, 1], torch.float64, seed=4)
+    out, lse = R.decode_paged(q, kv, table, lens, SCALE, dtype=torch.float64)
+    for b in range(2):
+        k0 = kv[table[b, 0].long(), 0, 0]
+        assert torch.allclose(out[b, 0], k0[:512].expand(16, -1), atol=1e-12)
+        assert torch.allclose(lse[b, :, 0], (q[b, 0] @ k0) * SCALE, atol=1e-12)
+
+
+def test_zero_query_is_uniform():
+    q, kv, table, lens = rand_paged(2, 1, 16, [37, 300], torch.float64, seed=5)
+    q.zero_()
+    out, lse = R.decode_paged(q, kv, table, lens, SCALE, dtype=torch.float64)
+    for b, L in enumerate([37, 300]):
+        k = R.gather(kv[:, :, 0], table[b], L)
+        assert torch.allclose(out[b, 0], k[:, :512].mean(0).expand(16, -1), atol=1e-12)
+        assert torch.allclose(lse[b, :, 0], torch.full((16,), math.log(L), dtype=torch.float64))
+
+
+def test_identical_keys():
+    q, kv, table, lens = rand_paged(1, 1, 16, [150], torch.float64, seed=6)
+    kv[:] = kv[0, 0]
+    out, lse = R.decode_paged(q, kv, table, lens, SCALE, dtype=torch.float64)
+    k = kv[0, 0, 0]
+    assert torch.allclose(out[0, 0], k[:512].expand(16, -1), atol=1e-12)
+    assert torch.allclose(lse[0, :, 0], q[0, 0] @ k * SCALE + math.log(150), atol=1e-12)
+
+
+def test_page_permutation_invariance():
+    q, kv, table, lens = rand_paged(2, 1, 16, [130, 250], seed=7)
+    out, lse = R.decode_paged(q, kv, table, lens, SCALE)
+    perm = torch.randperm(kv.shape[0], generator=torch.Generator().manual_seed(1))
+    inv = torch.argsort(perm)
+    out2, lse2 = R.decode_paged(q, kv[perm], inv[table.long()].to(torch.int32), lens, SCALE)
+    assert torch.allclose(out, out2, atol=1e-6) and torch.allclose(lse, lse2, atol=1e-6)
+
+
+def test_split_and_merge():
+    # two halves of the key set as two sequences, merged, equal the whole
+    q, kv, table, lens = rand_paged(1, 1, 16, [256], torch.float64, seed=8)
+    whole_o, whole_l = R.decode_paged(q, kv, table, lens, SCALE, dtype=torch.float64)
+    halves = torch.stack([table[0, :2], table[0, 2:4]])
+    o2, l2 = R.decode_paged(q.expand(2, -1, -1, -1), kv, halves, torch.tensor([128, 128]), SCALE,
+                            dtype=torch.float64)
+    mo, ml = R.combine(o2[:, 0], l2[:, :, 0])
+    assert torch.allclose(mo, whole_o[0, 0], atol=1e-12)
+    assert torch.allclose(ml, whole_l[0, :, 0], atol=1e-12)
+
+
+def test_query_scaling():
+    q, kv, table, lens = rand_paged(1, 1, 16, [99], torch.float64, seed=9)
+    o1, l1 = R.decode_paged(q, kv, table, lens, SCALE, dtype=torch.float64)
+    o2, l2 = R.decode_paged(q * 3.0, kv, table, lens, SCALE / 3.0, dtype=torch.float64)
+    assert torch.allclose(o1, o2, atol=1e-12) and torch.allclose(l1, l2, atol=1e-12)
+
+
+def test_causal_rows_match_single_query_decodes():
+    q, kv, table, lens = rand_paged(2, 2, 16, [1, 77], torch.float64, seed=10)
+    out, lse = R.decode_paged(q, kv, table, lens, SCALE, causal=True, dtype=torch.float64)
+    for i, shift in ((1, 0), (0, 1)):
+        lens_i = lens - shift
+        o1, l1 = R.decode_paged(q[:, i:i + 1], kv, table, lens_i, SCALE, dtype=torch.float64)
+        assert torch.allclose(out[:, i], o1[:, 0], atol=1e-12)
+        assert torch.equal(torch.isinf(lse[:, :, i]), torch.isinf(l1[:, :, 0]))
+    # L = 1 with s_q = 2: query 0 sees nothing
+    assert torch.all(out[0, 0] == 0) and torch.all(torch.isinf(lse[0, :, 0]))
+
+
+def test_contiguous_equals_identity_paged():
+    g = torch.Generator().manual_seed(11)
+    B, H, L = 2, 16, 128
+    q, q_pe = torch.randn(B, H, 512, generator=g), torch.randn(B, H, 64, generator=g)
+    kv, k_pe = torch.randn(B, L, 1, 512, generator=g), torch.randn(B, L, 1, 64, generator=g)
+    ref = R.decode_contiguous(q, q_pe, kv, k_pe)
+    cache = torch.cat([kv, k_pe], -1).reshape(B * L // 64, 64, 1, 576)
+    table = torch.arange(B * L // 64, dtype=torch.int32).reshape(B, -1)
+    out, _ = R.decode_paged(torch.cat([q, q_pe], -1).unsqueeze(1), cache, table,
+                            torch.full((B,), L, dtype=torch.int32), SCALE)
+    assert torch.allclose(out[:, 0], ref, atol=1e-5)
+
+
+def test_split_plan_bruteforce():
+    for L in list(range(1, 300, 7)) + [2048, 3000, 4095, 4096, 8192, 16384, 65536]:
+        for block_n in (16, 32, 64):
+            nb = -(-L // block_n)
+            for ns_req in (1, 2, 3, 7, 64, 104, 208, 312, 1024):
+                ns, bpc, extra = R.split_plan(L, ns_req, block_n, False)
+                assert extra == 0 and ns * bpc >= nb and (ns - 1) * bpc < nb
+                ns, bpc, extra = R.split_plan(L, ns_req, block_n, True)
+                assert ns == max(1, min(ns_req, nb)) and ns * bpc + extra == nb and extra < ns
+    # the reference's recorded best configs are coverable splits
+    assert R.split_plan(16384, 104, 32, True) == (104, 4, 96)
+    assert R.split_plan(8192, 312, 32, False)[0] == 256
+
+
+def _check_schedule(lengths, recs, prefix, num_parts):
+    segs = R.segments(recs, lengths)
+    covered = {}
+    for p, b, pb, pe, sp in segs:
+        for pg in range(pb, pe):
+            assert (b, pg) not in covered
+            covered[(b, pg)] = p
+        covered.setdefault(("seq", b), []).append(sp)
+    for b, L in enumerate(lengths):
+        for pg in range(R.pages_of(L)):
+            assert (b, pg) in covered
+        splits = covered[("seq", b)]
+        assert sorted(splits) == list(range(len(splits)))
+        assert prefix[b + 1] - prefix[b] == len(splits)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_balanced_schedule_bruteforce(seed):
+    rng = random.Random(seed)
+    B = rng.choice([1, 3, 17, 64, 132])
+    lengths = [rng.choice([0, 1, 63, 64, 65, rng.randint(1, 20000)]) for _ in range(B)]
+    for parts in (1, 7, 64, 256):
+        for fo in (0, 2, 5):
+            recs, prefix = R.schedule_balanced(lengths, parts, fo)
+            assert len(recs) == parts
+            _check_schedule(lengths, recs, prefix, parts)
+            total = sum(R.pages_of(L) + fo for L in lengths)
+            payload = -(-total // parts) + fo
+            for p, b, pb, pe, sp in R.segments(recs, lengths):
+                if p < parts - 1:
+                    assert pe - pb <= payload
+
+
+def test_forced_schedule_bruteforce():
+    lengths = [0, 1, 64, 65, 1000, 4096]
+    for forced in (1, 2, 3, 8):
+        recs, prefix = R.schedule_forced(lengths, forced)
+        assert len(recs) == len(lengths) * forced
+        _check_schedule(lengths, recs, prefix, len(recs))
+        for b, L in enumerate(lengths):
+            assert prefix[b + 1] - prefix[b] == max(1, min(forced, R.pages_of(L)))
+
+
+def test_oracle_mistakes_are_caught():
+    """A planted mistake in the oracle (dropping the rope dims) fails the fixture check."""
+    z = np.load(GOLDEN)
+    c = load_case(z, "h16_tails")
+    q = c["q"].clone()
+    q[..., 512:] = 0  # what an oracle that forgot q_rope . k_rope would compute
+    out, _ = R.decode_paged(q, c["kv"], c["table"], c["lengths"], SCALE, c["causal"])
+    assert not torch.allclose(out, c["out"], atol=2e-5, rtol=1e-4)
