@@ -33,6 +33,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline")
     ap.add_argument("--all-configs", action="store_true", help="also print one line per config to stderr")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run a plain MIB-MiB device copy 3x (scale for FETCH/WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -78,42 +80,29 @@ def measure(cfg_name, steps, warmup):
     out = torch.empty(B, s_q, H, 512, dtype=cfg.dtype, device="cuda:0")
     lse = torch.empty(B, H, s_q, dtype=torch.float32, device="cuda:0")
 
-    def call():
+    import ctypes
+    from mlc_decode_amd._lib import check
+    from mlc_decode_amd.api import make_decode_args
+    lib = _lib.load()
+    args, _, _, keep = make_decode_args(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                        sched, splits, inp.sm_scale, inp.causal, out, lse)
+    ap = ctypes.byref(args)
+    sp = stream.cuda_stream
+
+    def call():  # the public call path, validation and all
         flash_mla_with_kvcache(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, 512,
                                sched, splits, softmax_scale=inp.sm_scale, causal=inp.causal,
                                out=out, lse=lse)
 
-    # whole call: main split-KV kernel + combine
     ms_call = time_gpu(call, steps, warmup, stream)
-
-    # combine alone, re-run on the partials the last call left in the workspace
-    import ctypes
-    from mlc_decode_amd.api import workspace
-    from mlc_decode_amd._lib import MlaDecodeArgs, check
-    lib = _lib.load()
-    ws_bytes = lib.mla_workspace_bytes(B, s_q, H, sched.shape[0])
-    ws = workspace(inp.q.device, ws_bytes)
-    a = MlaDecodeArgs()
-    a.batch, a.s_q, a.heads_q, a.heads_k, a.dtype = B, s_q, H, 1, 0 if cfg.dtype == torch.bfloat16 else 1
-    a.causal, a.sm_scale, a.num_blocks = int(inp.causal), inp.sm_scale, inp.kv_cache.shape[0]
-    a.q_nope, a.q_rope = inp.q.data_ptr(), inp.q.data_ptr() + 1024
-    a.q_stride_b, a.q_stride_s, a.q_stride_h = inp.q.stride(0), inp.q.stride(1), inp.q.stride(2)
-    a.q_rope_stride_b, a.q_rope_stride_s, a.q_rope_stride_h = a.q_stride_b, a.q_stride_s, a.q_stride_h
-    a.kv_nope, a.kv_rope = inp.kv_cache.data_ptr(), inp.kv_cache.data_ptr() + 1024
-    a.kv_stride_page = a.kv_rope_stride_page = inp.kv_cache.stride(0)
-    a.kv_stride_tok = a.kv_rope_stride_tok = inp.kv_cache.stride(1)
-    a.block_table, a.block_table_stride = inp.block_table.data_ptr(), inp.block_table.stride(0)
-    a.num_parts = sched.shape[0]
-    a.cache_seqlens, a.tile_sched, a.num_splits = inp.cache_seqlens.data_ptr(), sched.data_ptr(), splits.data_ptr()
-    a.out, a.lse = out.data_ptr(), lse.data_ptr()
-    a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride(0), out.stride(1), out.stride(2)
-    a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
-    sp = stream.cuda_stream
-    ms_combine = time_gpu(lambda: check("mla_combine_fwd", lib.mla_combine_fwd(ctypes.byref(a), sp)),
+    # the two kernels separately, launched through the C ABI on the same stream
+    ms_main = time_gpu(lambda: check("mla_splitkv_fwd", lib.mla_splitkv_fwd(ap, sp)),
+                       steps, warmup, stream)
+    ms_combine = time_gpu(lambda: check("mla_combine_fwd", lib.mla_combine_fwd(ap, sp)),
                           steps, warmup, stream)
     ms_meta = time_gpu(lambda: get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=forced),
                        steps, warmup, stream)
-    ms_main = max(ms_call - ms_combine, 1e-6)
+    del keep
 
     nbytes = algorithmic_bytes(cpu_inp.cache_seqlens, B, s_q, H, 2)
     flops = algorithmic_flops(cpu_inp.cache_seqlens, s_q, H, cfg.causal)
@@ -172,6 +161,14 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20)
+        src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     m = measure(args.config, args.steps, args.warmup)
     cfg = m["cfg"]
     if args.all_configs:

@@ -19,6 +19,7 @@
  *                           (algorithm described in docs/num_split_design.md:31-135)
  *   - mla_decode_fwd        the flash_mla_with_kvcache call of handmade/bench_metax_flashmla.py:33-35,
  *                           and the main + combine TileLang kernels of mla_decode.py:78-259
+ *   - mla_splitkv_fwd       the main split-KV TileLang kernel alone, mla_decode.py:78-192
  *   - mla_combine_fwd       the combine kernel of mla_decode.py:194-246 (LSE-weighted merge)
  *   - mla_split_plan        _split_plan of mla_decode.py:9-30
  */
@@ -151,6 +152,13 @@ int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t
  * TileLang main + combine kernels (mla_decode.py:78-259).
  */
 int mla_decode_fwd(const mla_decode_args* args, void* stream);
+
+/*
+ * Main split-KV kernel alone (the first half of mla_decode_fwd): sequences with a single
+ * split are finished (out, lse); the partials of split sequences are left in `workspace`
+ * for mla_combine_fwd.  Replaces the main TileLang kernel of mla_decode.py:78-192.
+ */
+int mla_splitkv_fwd(const mla_decode_args* args, void* stream);
 
 /*
  * Combine stage alone, over partials produced by mla_decode_fwd into `workspace`

@@ -28,6 +28,7 @@ EXPORTED = (
     "mla_get_metadata_host",
     "mla_workspace_bytes",
     "mla_decode_fwd",
+    "mla_splitkv_fwd",
     "mla_combine_fwd",
     "mla_merge_partials",
     "mla_split_plan",
@@ -124,6 +125,8 @@ def load() -> ctypes.CDLL:
         lib.mla_workspace_bytes.restype = ctypes.c_int64
         lib.mla_decode_fwd.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]
         lib.mla_decode_fwd.restype = ctypes.c_int
+        lib.mla_splitkv_fwd.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]
+        lib.mla_splitkv_fwd.restype = ctypes.c_int
         lib.mla_combine_fwd.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]
         lib.mla_combine_fwd.restype = ctypes.c_int
         lib.mla_merge_partials.argtypes = [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]

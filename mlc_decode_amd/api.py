@@ -123,9 +123,15 @@ def _split_kv(kv_cache) -> Tuple[torch.Tensor, torch.Tensor]:
     return kv_cache[..., :MLA_DIM_V], kv_cache[..., MLA_DIM_V:]
 
 
-def _decode(q: torch.Tensor, kv_cache, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
-            sched: torch.Tensor, splits: torch.Tensor, sm_scale: float, causal: bool,
-            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
+                     cache_seqlens: torch.Tensor, sched: torch.Tensor, splits: torch.Tensor,
+                     sm_scale: float, causal: bool, out: Optional[torch.Tensor] = None,
+                     lse: Optional[torch.Tensor] = None):
+    """Validate a paged decode and fill the C ``mla_decode_args`` for it.
+
+    Returns ``(args, out, lse, keep)``; ``keep`` holds the tensors the args point into and
+    must stay alive while the args are used.
+    """
     _require_gpu(q, "q")
     if q.dim() != 4 or q.shape[-1] != MLA_DIM_QK:
         raise ValueError(f"q must be [B, s_q, H, {MLA_DIM_QK}]")
@@ -153,6 +159,8 @@ def _decode(q: torch.Tensor, kv_cache, block_table: torch.Tensor, cache_seqlens:
         lse = torch.empty(B, H, s_q, dtype=torch.float32, device=q.device)
     if lse.shape != (B, H, s_q) or not lse.is_contiguous() or lse.dtype != torch.float32:
         raise ValueError("lse must be a contiguous fp32 [B, H, s_q] tensor")
+    if out.shape != (B, s_q, H, MLA_DIM_V) or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must be [B, s_q, H, 512] in q's dtype with unit last stride")
     seqlens = cache_seqlens.contiguous()
     sched = sched.contiguous()
     splits = splits.contiguous()
@@ -185,7 +193,16 @@ def _decode(q: torch.Tensor, kv_cache, block_table: torch.Tensor, cache_seqlens:
     a.lse = lse.data_ptr()
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws_bytes
-    check("mla_decode_fwd", lib.mla_decode_fwd(ctypes.byref(a), _stream_ptr(q.device)))
+    keep = (q, latent, rope, block_table, seqlens, sched, splits, out, lse, ws)
+    return a, out, lse, keep
+
+
+def _decode(q, kv_cache, block_table, cache_seqlens, sched, splits, sm_scale, causal,
+            out=None, lse=None):
+    a, out, lse, keep = make_decode_args(q, kv_cache, block_table, cache_seqlens, sched, splits,
+                                         sm_scale, causal, out, lse)
+    check("mla_decode_fwd", _lib.load().mla_decode_fwd(ctypes.byref(a), _stream_ptr(q.device)))
+    del keep
     return out, lse
 
 

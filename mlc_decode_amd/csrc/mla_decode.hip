@@ -24,14 +24,15 @@
 //                                                    the same LDS stage (V is never
 //                                                    copied or re-read from HBM)
 // so the only cross-lane work is the row max / row sum over 4 lane groups.
-// Online softmax uses a lazily rescaled reference max: O and the row sums are rescaled
-// only when a row's stage max exceeds the reference by more than 2^8, which keeps every
-// P <= 256 (exact in fp32 sums, no bf16/f16 overflow) and skips almost all rescales.
+// The softmax reference max is fixed per segment from its first stage (see ref_tau), so the
+// output accumulators are never rescaled; a score far above it triggers an exact two-pass
+// redo of the segment.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "mla_decode_amd.h"
 #include "mla_sched.h"
@@ -49,7 +50,6 @@ constexpr int kLoadsPerStage = kStageBytes / 1024;     // 36 wave-wide 16-byte l
 constexpr int kPanelBytes = kStageBytes / 2;           // 16 token rows
 constexpr int kKSteps = kDQK / 32;                     // 18 k-steps of the QK product
 constexpr int kDimTiles = kDV / 16;                    // 32 output dim tiles
-constexpr float kTau = 8.0f;                           // lazy-rescale threshold (log2 units)
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -107,6 +107,30 @@ __device__ __forceinline__ f32x4 mfma32(i32x4 a, i32x4 b, f32x4 c) {
   }
 }
 
+// The QK accumulators are kept in VGPRs through inline asm: at one wave per SIMD the compiler
+// selects the AGPR form for every MFMA builtin, and the 32-row tile's output accumulator
+// (256 registers) already fills the AGPR file.  Operands come straight from LDS / global
+// loads; the chain is volatile so no compiler VALU lands between its MFMAs, and
+// qk_settle() adds the wait states an MFMA result needs before a VALU may read it.
+template <int DT>
+__device__ __forceinline__ void mfma_qk_first(f32x4& acc, const i32x4& a, const i32x4& b) {
+  if constexpr (DT == MLA_DTYPE_BF16)
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
+}
+template <int DT>
+__device__ __forceinline__ void mfma_qk(f32x4& acc, const i32x4& a, const i32x4& b) {
+  if constexpr (DT == MLA_DTYPE_BF16)
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void qk_settle(f32x4& acc) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(acc));
+}
+__device__ __forceinline__ void qk_touch(f32x4& acc) { asm volatile("" : "+v"(acc)); }
+
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
   if constexpr (DT == MLA_DTYPE_BF16) {
@@ -131,20 +155,28 @@ __device__ __forceinline__ float to_f32(uint16_t v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// One wave-wide 16-byte-per-lane HBM -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes
-// land at LDS byte lds_addr + 16*l.  Issued as inline asm on purpose: the compiler then does
-// not track it as an LDS store, so it adds no conservative vmcnt(0) waits before the LDS
-// reads of *other* stages; completion is awaited explicitly (wait_stage) before a barrier.
-// M0 (the LDS base of the copy) is saved and restored around it.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
+// One wave-wide 16-byte-per-lane HBM -> LDS copy (global_load_lds_dwordx4, SGPR-base form):
+// lane l reads base + voff_l and its 16 bytes land at LDS byte lds_addr + 16*l.  Issued as
+// inline asm on purpose: the compiler then does not track it as an LDS store, so it adds no
+// conservative vmcnt(0) waits before the LDS reads of *other* stages; completion is awaited
+// explicitly (wait_stage) before a barrier.  M0 (the LDS base of the copy) is saved and
+// restored around it.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds_addr) {
+  // base and lds_addr are uniform; readfirstlane makes that visible to the register allocator.
+  // The builtin returns a signed int: each half goes through uint32_t before widening, or a
+  // low word with bit 31 set would sign-extend into the high word.
+  const uint64_t b64 = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b64);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b64 >> 32));
+  const uint64_t sbase = ((uint64_t)hi << 32) | (uint64_t)lo;
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+      : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
       : "memory");
 }
 
@@ -185,21 +217,22 @@ __device__ __forceinline__ void issue_stage(uint8_t LDS_AS* slot, const uint16_t
                                             const uint16_t* rope_base, int kv_st, int kr_st,
                                             int last_row, int wave, int lane) {
   const int prow = (lane & 15) ^ (((lane >> 4) & 1) << 3);
-  const int cl = (lane >> 4) * 8;  // element offset of the lane's chunk inside a load
+  const uint32_t cl = (uint32_t)(lane >> 4) * 16;  // byte offset of the lane's chunk in a load
+  // Rows past the sequence end re-read its last row: in bounds, finite, masked later.
   const int r0 = prow < last_row ? prow : last_row;
   const int r1 = prow + 16 < last_row ? prow + 16 : last_row;
-  // Rows past the sequence end re-read its last row: in bounds, finite, masked later.
-  const uint16_t* n0 = nope_base + (r0 * kv_st + cl);
-  const uint16_t* n1 = nope_base + (r1 * kv_st + cl);
-  const uint16_t* q0 = rope_base + (r0 * kr_st + cl);
-  const uint16_t* q1 = rope_base + (r1 * kr_st + cl);
+  const uint32_t on0 = (uint32_t)(r0 * kv_st) * 2 + cl, on1 = (uint32_t)(r1 * kv_st) * 2 + cl;
+  const uint32_t or0 = (uint32_t)(r0 * kr_st) * 2 + cl, or1 = (uint32_t)(r1 * kr_st) * 2 + cl;
 #pragma unroll
   for (int j = 0; j < kLoadsPerStage / NW; ++j) {
-    const int i = wave + NW * j;  // NW divides 36, so i's panel and chunk are known per wave
+    const int i = wave + NW * j;  // wave is uniform, so the panel / rope choice is scalar
     const int panel = i >= 18;
     const int ii = i - 18 * panel;
-    const uint16_t* src = ii < 16 ? (panel ? n1 : n0) + 32 * ii : (panel ? q1 : q0) + 32 * (ii - 16);
-    dma16(src, (uint32_t)(uintptr_t)(slot + i * 1024));
+    if (ii < 16)
+      dma16((const char*)nope_base + 64 * ii, panel ? on1 : on0, (uint32_t)(uintptr_t)(slot + i * 1024));
+    else
+      dma16((const char*)rope_base + 64 * (ii - 16), panel ? or1 : or0,
+            (uint32_t)(uintptr_t)(slot + i * 1024));
   }
 }
 
@@ -230,6 +263,24 @@ __device__ __forceinline__ i32x4 lds_tr_pair(const uint8_t LDS_AS* p) {
 // ---------------------------------------------------------------------------------------
 // main split-KV kernel
 // ---------------------------------------------------------------------------------------
+// Softmax reference.  A segment (the run of pages of one sequence a part owns) fixes its
+// reference row max m from the scores of its first stage; every later P = 2^(s*c - m) then
+// stays below 2^tau, which is finite in the 16-bit type P is rounded to and leaves fp32
+// sums far from overflow, so the output accumulators are never rescaled.  Should a later
+// score exceed m + tau, the whole workgroup abandons the pass and redoes the segment in two
+// passes: one that only finds the exact row max, one that accumulates against it.
+template <int DT>
+constexpr float ref_tau() {
+  return DT == MLA_DTYPE_BF16 ? 64.f : 15.f;
+}
+
+enum PassMode { kPassFirstStageRef = 0, kPassRowMax = 1, kPassFixedRef = 2 };
+
+__device__ __forceinline__ void wait_lgkm0() {
+  // lgkmcnt(0), vmcnt / expcnt left at their maxima
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+}
+
 template <int DT, int NW, int HT, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
   static_assert((NSTAGE - 2) * (kLoadsPerStage / NW) < 64, "vmcnt would overflow");
@@ -237,12 +288,20 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
   constexpr int R = NW * 16 * HT;
   constexpr int DK = 4;  // LDS prefetch depth of the QK A fragments
   constexpr int DV = 4;  // LDS prefetch depth of the PV A fragments
+  // With two row tiles per wave the last QL k-steps of the query (the rope dims) live in LDS,
+  // read back each stage just before use, to keep the loop inside the register file.
+  constexpr int QL = HT == 2 ? 2 : 0;
+  constexpr int QR = kKSteps - QL;  // k-steps of the query held in VGPRs
+  constexpr float kTau = ref_tau<DT>();
   __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[NSTAGE * kStageBytes];
+  __shared__ __attribute__((aligned(16))) i32x4 qtail_sh[QL > 0 ? NW * HT * QL * 64 : 1];
+  __shared__ int flag_sh[2][NW];  // per-wave "score above reference" flags, by stage parity
   uint8_t LDS_AS* smem = (uint8_t LDS_AS*)smem_raw;
 
   const int part = blockIdx.x;
   const int hb = blockIdx.y;
-  const int wave = threadIdx.x >> 6;
+  // wave index made explicitly uniform, so per-wave choices compile to scalar code
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;   // lane group (MFMA k quarter / output row quarter)
   const int li = lane & 15;  // lane within group
@@ -256,8 +315,13 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
   int split = rec[4];
 
   // Per-lane LDS byte offsets that do not depend on the stage (panel layout above).
-  // QK A operand, fragment (kk, tt): token row 16*tt + li, chunk 4*kk + g.
-  const int k_lane = g * 256 + ((li ^ ((g & 1) << 3)) << 4);
+  // QK A operand, fragment (kk, tt): token row 16*tt + li of chunk sigma(kk, g), where
+  //   sigma(kk, g) = 8*(kk/2) + 2*g + kk%2
+  // permutes the contraction order so that the four lane groups of one read see chunks of
+  // the same parity: the row XOR (8 on odd chunks) is then uniform across the read, which
+  // ds_read_b128 needs to stay conflict-free (the query fragments use the same sigma).
+  const int k_lane0 = (2 * g) * 256 + (li << 4);
+  const int k_lane1 = (2 * g + 1) * 256 + ((li ^ 8) << 4);
   // V^T A operand, dim tile dt: the lane addresses token row 4g + li/4 (and the same row of
   // the second panel), bytes 32*dt + 8*(li%4), i.e. chunk 2*dt + (li%4)/2.
   const int v_lane = ((li >> 1) & 1) * 256 + (((4 * g + (li >> 2)) ^ (((li >> 1) & 1) << 3)) << 4) +
@@ -279,7 +343,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
 
     // ---- query fragments (B operand of S^T = K Q^T), resident for the segment.  Rows
     // past the end re-load the last row; their results are never written.
-    i32x4 qf[HT][kKSteps];
+    i32x4 qf[HT][QR];
     int lim[HT];
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
@@ -288,166 +352,234 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
       const int s = row / p.heads;
       const int h = row - s * p.heads;
       lim[ht] = L - (p.causal ? (p.s_q - 1 - s) : 0);
-      const uint16_t* qn = p.q_nope + (b * p.q_sb + s * p.q_ss + h * p.q_sh) + 8 * g;
-      const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 8 * g;
+      const uint16_t* qn = p.q_nope + (b * p.q_sb + s * p.q_ss + h * p.q_sh) + 16 * g;
+      const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 16 * g;
 #pragma unroll
-      for (int kk = 0; kk < kKSteps; ++kk)
-        qf[ht][kk] = *(const i32x4*)(32 * kk < kRopeOff ? qn + 32 * kk : qr + (32 * kk - kRopeOff));
+      for (int kk = 0; kk < kKSteps; ++kk) {
+        // dims 8*sigma(kk, g) = 64*(kk/2) + 16*g + 8*(kk%2)
+        const int d = 64 * (kk >> 1) + 8 * (kk & 1);
+        const i32x4 v = *(const i32x4*)(d < kRopeOff ? qn + d : qr + (d - kRopeOff));
+        if (kk < QR)
+          qf[ht][kk < QR ? kk : 0] = v;
+        else
+          qtail_sh[((wave * HT + ht) * (QL > 0 ? QL : 1) + (kk - QR)) * 64 + lane] = v;
+      }
     }
     const int lmin = L - (p.causal ? p.s_q - 1 : 0);  // every row sees tokens < lmin
 
-    // ---- page-table cache: lane i holds the page id of page (pbase + i)
-    int pbase = page;
-    int bt_lane = 0;
-    if (paged) {
-      const int pi = pbase + lane;
-      int v = pi < np ? p.block_table[(int64_t)b * p.bt_stride + pi] : 0;
-      bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
-    }
-    wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
-
     f32x4 o[kDimTiles][HT];
-#pragma unroll
-    for (int dt = 0; dt < kDimTiles; ++dt)
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) o[dt][ht] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_ref[HT], l_part[HT];
-#pragma unroll
-    for (int ht = 0; ht < HT; ++ht) {
-      m_ref[ht] = -INFINITY;
-      l_part[ht] = 0.f;
-    }
+    int pbase = 0, bt_lane = 0;
 
-#define MLA_ISSUE(KIDX)                                                                        \
-  do {                                                                                         \
-    const int st_ = st_begin + (KIDX);                                                         \
-    const uint16_t* nb_;                                                                       \
-    const uint16_t* rb_;                                                                       \
-    if (paged) {                                                                               \
-      const int pidx_ = st_ >> 1;                                                              \
-      if (pidx_ - pbase >= 64) {                                                               \
-        pbase = pidx_;                                                                         \
-        const int pi_ = pbase + lane;                                                          \
-        int v_ = pi_ < np ? p.block_table[(int64_t)b * p.bt_stride + pi_] : 0;                 \
-        bt_lane = v_ < 0 ? 0 : (v_ >= p.num_blocks ? p.num_blocks - 1 : v_);                   \
-      }                                                                                        \
-      const int pg_ = __builtin_amdgcn_readlane(bt_lane, pidx_ - pbase);                       \
-      const int tok_ = (st_ & 1) * kStageTok;                                                  \
-      nb_ = p.kv_nope + ((int64_t)pg_ * p.kv_sp + tok_ * kv_st);                               \
-      rb_ = p.kv_rope + ((int64_t)pg_ * p.kr_sp + tok_ * kr_st);                               \
-    } else {                                                                                   \
-      nb_ = p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st_ * kStageTok * kv_st);             \
-      rb_ = p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st_ * kStageTok * kr_st);             \
-    }                                                                                          \
-    const int left_ = L - st_ * kStageTok;                                                     \
-    issue_stage<NW>(smem + ((KIDX) % NSTAGE) * kStageBytes, nb_, rb_, kv_st, kr_st,            \
-                    (left_ < kStageTok ? left_ : kStageTok) - 1, wave, lane);                  \
-  } while (0)
-
-#pragma unroll
-    for (int k = 0; k < NSTAGE - 1; ++k)
-      if (k < nst) MLA_ISSUE(k);
-
-#pragma unroll 1
-    for (int k = 0; k < nst; ++k) {
-      const int remaining_after = nst - 1 - k;
-      wait_stage<NW, NSTAGE>(remaining_after < NSTAGE - 2 ? remaining_after : NSTAGE - 2);
-      lds_barrier();
-      if (k + NSTAGE - 1 < nst) MLA_ISSUE(k + NSTAGE - 1);
-
-      const uint8_t LDS_AS* sb = smem + (k % NSTAGE) * kStageBytes;
-      const int st = st_begin + k;
-
-      // ---- S^T = K Q^T over 576 dims: two 16-token tiles x HT 16-row tiles.
-      // Fragment n = 2*kk + tt; DK fragments in flight ahead of the MFMAs.
-      f32x4 acc[HT][2];
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) acc[ht][0] = acc[ht][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      i32x4 kf[DK];
-#define MLA_KFRAG(N) (*(const i32x4 LDS_AS*)(sb + k_lane + ((N) & 1) * kPanelBytes + ((N) >> 1) * 1024))
-#pragma unroll
-      for (int n = 0; n < DK; ++n) kf[n] = MLA_KFRAG(n);
-#pragma unroll
-      for (int n = 0; n < 2 * kKSteps; ++n) {
-        const i32x4 a = kf[n % DK];
-        if (n + DK < 2 * kKSteps) kf[n % DK] = MLA_KFRAG(n + DK);
-#pragma unroll
-        for (int ht = 0; ht < HT; ++ht)
-          acc[ht][n & 1] = mfma32<DT>(a, qf[ht][n >> 1], acc[ht][n & 1]);
-        __builtin_amdgcn_sched_barrier(0);
+    auto load_page_ids = [&](int first) __attribute__((always_inline)) {
+      // lane i holds the page id of page (first + i); ids are clamped into the pool
+      pbase = first;
+      if (paged) {
+        const int pi = pbase + lane;
+        int v = pi < np ? p.block_table[(int64_t)b * p.bt_stride + pi] : 0;
+        bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
       }
-#undef MLA_KFRAG
+    };
 
-      // ---- mask tokens past each row's limit (sequence tail / causal)
-      if (st * kStageTok + kStageTok > lmin) {
+    auto issue = [&](int k) __attribute__((always_inline)) {
+      const int st = st_begin + k;
+      const uint16_t* nb;
+      const uint16_t* rb;
+      if (paged) {
+        const int pidx = st >> 1;
+        if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
+        const int pg = __builtin_amdgcn_readlane(bt_lane, pidx - pbase);
+        const int tok = (st & 1) * kStageTok;
+        nb = p.kv_nope + ((int64_t)pg * p.kv_sp + tok * kv_st);
+        rb = p.kv_rope + ((int64_t)pg * p.kr_sp + tok * kr_st);
+      } else {
+        nb = p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st * kStageTok * kv_st);
+        rb = p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st);
+      }
+      const int left = L - st * kStageTok;
+      issue_stage<NW>(smem + (k % NSTAGE) * kStageBytes, nb, rb, kv_st, kr_st,
+                      (left < kStageTok ? left : kStageTok) - 1, wave, lane);
+    };
+
+    // One pass over the segment's stages.  Returns true (uniformly across the workgroup)
+    // when a first-stage-reference pass saw a score above its reference by more than tau.
+    auto run_pass = [&](auto mode_tag) __attribute__((always_inline)) -> bool {
+      constexpr int MODE = decltype(mode_tag)::value;
+      if constexpr (MODE != kPassRowMax) {
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht)
+        for (int dt = 0; dt < kDimTiles; ++dt)
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) o[dt][ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) l_part[ht] = 0.f;
+      }
+      if constexpr (MODE != kPassFixedRef) {
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) m_ref[ht] = -INFINITY;
+      }
+      load_page_ids(page);
+      wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
+
+#pragma unroll
+      for (int k = 0; k < NSTAGE - 1; ++k)
+        if (k < nst) issue(k);
+
+      bool abort = false;
+#pragma unroll 1
+      for (int k = 0; k < nst; ++k) {
+        const int remaining_after = nst - 1 - k;
+        wait_stage<NW, NSTAGE>(remaining_after < NSTAGE - 2 ? remaining_after : NSTAGE - 2);
+        lds_barrier();
+        if constexpr (MODE == kPassFirstStageRef) {
+          if (k > 0) {
+            int any = 0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) any |= flag_sh[(k - 1) & 1][w];
+            if (any) {
+              abort = true;
+              break;
+            }
+          }
+        }
+        if (k + NSTAGE - 1 < nst) issue(k + NSTAGE - 1);
+
+        const uint8_t LDS_AS* sb = smem + (k % NSTAGE) * kStageBytes;
+        const int st = st_begin + k;
+
+        // ---- S^T = K Q^T over 576 dims: two 16-token tiles x HT 16-row tiles.
+        // Fragment n = 2*kk + tt; DK fragments in flight ahead of the MFMAs.
+        f32x4 acc[HT][2];
+        i32x4 kf[DK];
+        i32x4 qt[HT][QL > 0 ? QL : 1];
+#define MLA_KFRAG(N) \
+  (*(const i32x4 LDS_AS*)(sb + (((N) >> 1) & 1 ? k_lane1 : k_lane0) + ((N) & 1) * kPanelBytes + ((N) >> 2) * 2048))
+#pragma unroll
+        for (int n = 0; n < DK; ++n) kf[n] = MLA_KFRAG(n);
+#pragma unroll
+        for (int n = 0; n < 2 * kKSteps; ++n) {
+          const i32x4 a = kf[n % DK];
+          if (n + DK < 2 * kKSteps) kf[n % DK] = MLA_KFRAG(n + DK);
+          if (QL > 0 && n == 2 * QR - DK) {  // query tail, DK fragments ahead of its use
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+              for (int j = 0; j < (QL > 0 ? QL : 1); ++j)
+                qt[ht][j] = qtail_sh[((wave * HT + ht) * (QL > 0 ? QL : 1) + j) * 64 + lane];
+          }
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) {
+            const int kk = n >> 1;
+            const i32x4 qb = kk < QR ? qf[ht][kk < QR ? kk : 0] : qt[ht][kk < QR ? 0 : kk - QR];
+            if (n < 2)
+              mfma_qk_first<DT>(acc[ht][n & 1], a, qb);
+            else
+              mfma_qk<DT>(acc[ht][n & 1], a, qb);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#undef MLA_KFRAG
+        qk_settle(acc[0][0]);
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          if (ht > 0) qk_touch(acc[ht][0]);
+          qk_touch(acc[ht][1]);
+        }
+
+        // ---- mask tokens past each row's limit (sequence tail / causal)
+        if (st * kStageTok + kStageTok > lmin) {
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int t = st * kStageTok + 16 * tt + 4 * g + r;
+                if (t >= lim[ht]) acc[ht][tt][r] = -INFINITY;
+              }
+        }
+
+        // ---- this lane's largest scaled score per row tile
+        float lmx[HT];
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          const float v = fmaxf(fmaxf(fmaxf(acc[ht][0][0], acc[ht][0][1]), fmaxf(acc[ht][0][2], acc[ht][0][3])),
+                                fmaxf(fmaxf(acc[ht][1][0], acc[ht][1][1]), fmaxf(acc[ht][1][2], acc[ht][1][3])));
+          lmx[ht] = v * p.scale_log2;
+        }
+        if constexpr (MODE == kPassRowMax) {
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) m_ref[ht] = fmaxf(m_ref[ht], lmx[ht]);
+          continue;
+        }
+        if constexpr (MODE == kPassFirstStageRef) {
+          if (k == 0) {
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) m_ref[ht] = wave_max_g(lmx[ht]);
+            if (lane == 0) flag_sh[0][wave] = 0;
+          } else {
+            bool over = false;
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
+            const bool any = __builtin_amdgcn_ballot_w64(over) != 0;
+            if (lane == 0) flag_sh[k & 1][wave] = any ? 1 : 0;
+          }
+        }
+
+        // ---- P^T = 2^(S^T * sm_scale * log2(e) - m), packed to the B operand of PV
+        i32x4 pb[HT];
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          const float mu = m_ref[ht] == -INFINITY ? 0.f : m_ref[ht];
+          float pv[2][4];
+          float sum = 0.f;
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int t = st * kStageTok + 16 * tt + 4 * g + r;
-              if (t >= lim[ht]) acc[ht][tt][r] = -INFINITY;
+              pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
+              sum += pv[tt][r];
             }
-      }
-
-      // ---- online softmax with a lazily moved reference max
-      float mx[HT];
-      bool need_any = false;
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) {
-        const float v = fmaxf(fmaxf(fmaxf(acc[ht][0][0], acc[ht][0][1]), fmaxf(acc[ht][0][2], acc[ht][0][3])),
-                              fmaxf(fmaxf(acc[ht][1][0], acc[ht][1][1]), fmaxf(acc[ht][1][2], acc[ht][1][3])));
-        mx[ht] = wave_max_g(v) * p.scale_log2;
-        need_any |= mx[ht] > m_ref[ht] + kTau;
-      }
-      if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
-#pragma unroll
-        for (int ht = 0; ht < HT; ++ht) {
-          const bool need = mx[ht] > m_ref[ht] + kTau;
-          const float m_new = need ? mx[ht] : m_ref[ht];
-          const float alpha = need ? fast_exp2(m_ref[ht] - m_new) : 1.f;
-          m_ref[ht] = m_new;
-          l_part[ht] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < kDimTiles; ++dt) o[dt][ht] *= alpha;
+          l_part[ht] += sum;
+          pb[ht] = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
+                         (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
         }
-      }
-      i32x4 pb[HT];
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) {
-        const float mu = m_ref[ht] == -INFINITY ? 0.f : m_ref[ht];
-        float pv[2][4];
-        float sum = 0.f;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
-            sum += pv[tt][r];
-          }
-        l_part[ht] += sum;
-        pb[ht] = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
-                       (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
-      }
 
-      // ---- O^T += V^T P^T over the 32 tokens of the stage; DV fragments in flight
-      i32x4 vf[DV];
+        // ---- O^T += V^T P^T over the 32 tokens of the stage; DV fragments in flight
+        i32x4 vf[DV];
 #define MLA_VFRAG(DTI) lds_tr_pair(sb + v_lane + (DTI) * 512)
 #pragma unroll
-      for (int n = 0; n < DV; ++n) vf[n] = MLA_VFRAG(n);
+        for (int n = 0; n < DV; ++n) vf[n] = MLA_VFRAG(n);
 #pragma unroll
-      for (int dt = 0; dt < kDimTiles; ++dt) {
-        const i32x4 a = vf[dt % DV];
-        if (dt + DV < kDimTiles) vf[dt % DV] = MLA_VFRAG(dt + DV);
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          const i32x4 a = vf[dt % DV];
+          if (dt + DV < kDimTiles) vf[dt % DV] = MLA_VFRAG(dt + DV);
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht) o[dt][ht] = mfma32<DT>(a, pb[ht], o[dt][ht]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+          for (int ht = 0; ht < HT; ++ht) o[dt][ht] = mfma32<DT>(a, pb[ht], o[dt][ht]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
 #undef MLA_VFRAG
+        if constexpr (MODE == kPassFirstStageRef) wait_lgkm0();  // flag store lands before the barrier
+      }
+      if constexpr (MODE == kPassFirstStageRef) {
+        if (!abort && nst > 1) {  // the last stage's flags
+          lds_barrier();
+          int any = 0;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) any |= flag_sh[(nst - 1) & 1][w];
+          abort = any != 0;
+        }
+      }
+      wait_vmcnt<0>();  // an abandoned pass may leave stage loads in flight
+      lds_barrier();    // every wave is done with the LDS ring before it is refilled
+      return abort;
+    };
+
+    if (run_pass(std::integral_constant<int, kPassFirstStageRef>{})) {
+      run_pass(std::integral_constant<int, kPassRowMax>{});
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) m_ref[ht] = wave_max_g(m_ref[ht]);
+      run_pass(std::integral_constant<int, kPassFixedRef>{});
     }
-#undef MLA_ISSUE
-    lds_barrier();  // every wave is done with the LDS ring before it is refilled
 
     // ---- epilogue: finish the row sums, normalise, write final or partial output
     const int slot0 = p.splits[b];
@@ -464,9 +596,10 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
       if (single) {
         uint16_t* dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 4 * g;
 #pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) {
+        for (int dt = 0; dt < kDimTiles; ++dt) {  // one tile at a time (register pressure)
           const f32x4 v = o[dt][ht] * inv;
           *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
+          __builtin_amdgcn_sched_barrier(0);
         }
         if (g == 0 && p.lse != nullptr)
           p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
@@ -474,7 +607,10 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         const int64_t slot = slot0 + split;
         float* dst = p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
 #pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) *(f32x4*)(dst + 16 * dt) = o[dt][ht] * inv;
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          *(f32x4*)(dst + 16 * dt) = o[dt][ht] * inv;
+          __builtin_amdgcn_sched_barrier(0);
+        }
         if (g == 0) p.ws_lse[slot * p.rows + row] = lse2;
       }
     }
@@ -580,9 +716,8 @@ struct Variant {
   int nw, ht, nstage;
 };
 
-// Rows per workgroup R = nw*16*ht; LDS per workgroup nstage*36 KiB.  Every variant keeps
-// one 16-row tile per wave (ht = 1): the query tile (72 VGPRs) and the fp32 output tile
-// (128 AGPRs) of a wave then fit the register file without spills.
+// Rows per workgroup R = nw*16*ht; LDS per workgroup nstage*36 KiB.  A wave owns one 16-row
+// tile; above 64 rows the rows are split over ceil(rows/64) head blocks (grid dimension y).
 Variant pick_variant(int rows) {
   if (rows <= 16) return {1, 1, 3};
   if (rows <= 32) return {2, 1, 3};
@@ -648,6 +783,10 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
                         a->q_rope_stride_s, a->q_rope_stride_h, a->kv_stride_tok, a->kv_rope_stride_tok};
   for (int64_t s : s8)
     if (s < 0 || s % 8) return fail(MLA_ERR_INVALID, "q/kv strides must be non-negative multiples of 8 elements");
+  // The kernel forms each lane's byte offset inside a 32-token stage in 32 bits (SGPR base
+  // + 32-bit VGPR offset): 63 * stride * 2 bytes must stay far below 2^31.
+  if (a->kv_stride_tok >= (int64_t(1) << 24) || a->kv_rope_stride_tok >= (int64_t(1) << 24))
+    return fail(MLA_ERR_UNSUPPORTED, "kv token strides must be below 2^24 elements");
   if (a->block_table) {
     if (a->kv_stride_page < 0 || a->kv_stride_page % 8 || a->kv_rope_stride_page < 0 || a->kv_rope_stride_page % 8)
       return fail(MLA_ERR_INVALID, "page strides must be non-negative multiples of 8 elements");
@@ -785,6 +924,12 @@ int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t
 }
 
 int mla_decode_fwd(const mla_decode_args* args, void* stream) {
+  const int rc = mla_splitkv_fwd(args, stream);
+  if (rc != MLA_OK) return rc;
+  return launch_combine(make_params(args), args->dtype, 0, (hipStream_t)stream);
+}
+
+int mla_splitkv_fwd(const mla_decode_args* args, void* stream) {
   int64_t need = 0;
   const int rc = validate(args, &need);
   if (rc != MLA_OK) return rc;
@@ -792,12 +937,11 @@ int mla_decode_fwd(const mla_decode_args* args, void* stream) {
   const Variant v = pick_variant(kp.rows);
   const int R = v.nw * 16 * v.ht;
   const int head_blocks = (kp.rows + R - 1) / R;
-  hipStream_t st = (hipStream_t)stream;
   const hipError_t e = args->dtype == MLA_DTYPE_BF16
-                           ? launch_main_dt<MLA_DTYPE_BF16>(v, kp, head_blocks, st)
-                           : launch_main_dt<MLA_DTYPE_F16>(v, kp, head_blocks, st);
+                           ? launch_main_dt<MLA_DTYPE_BF16>(v, kp, head_blocks, (hipStream_t)stream)
+                           : launch_main_dt<MLA_DTYPE_F16>(v, kp, head_blocks, (hipStream_t)stream);
   if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("decode launch failed: ") + hipGetErrorString(e));
-  return launch_combine(kp, args->dtype, 0, st);
+  return MLA_OK;
 }
 
 int mla_combine_fwd(const mla_decode_args* args, void* stream) {
