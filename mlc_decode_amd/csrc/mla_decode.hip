@@ -126,10 +126,21 @@ __device__ __forceinline__ void mfma_qk(f32x4& acc, const i32x4& a, const i32x4&
   else
     asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
 }
+// 32 wait states after the last QK MFMA: covers the MFMA-result -> VALU-read latency and the
+// passes during which the last MFMAs still read their A/B operands.
 __device__ __forceinline__ void qk_settle(f32x4& acc) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(acc));
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc));
 }
 __device__ __forceinline__ void qk_touch(f32x4& acc) { asm volatile("" : "+v"(acc)); }
+
+// 32 wait states during which the MFMA source operands passed in stay untouched.
+template <int HT>
+__device__ __forceinline__ void operand_guard(i32x4 (&pb)[HT], i32x4& va) {
+  if constexpr (HT == 2)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(pb[0]), "+v"(pb[1]), "+v"(va));
+  else
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(pb[0]), "+v"(va));
+}
 
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
@@ -288,14 +299,11 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
   constexpr int R = NW * 16 * HT;
   constexpr int DK = 4;  // LDS prefetch depth of the QK A fragments
   constexpr int DV = 4;  // LDS prefetch depth of the PV A fragments
-  // With two row tiles per wave the last QL k-steps of the query (the rope dims) live in LDS,
-  // read back each stage just before use, to keep the loop inside the register file.
-  constexpr int QL = HT == 2 ? 2 : 0;
-  constexpr int QR = kKSteps - QL;  // k-steps of the query held in VGPRs
   constexpr float kTau = ref_tau<DT>();
   __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[NSTAGE * kStageBytes];
-  __shared__ __attribute__((aligned(16))) i32x4 qtail_sh[QL > 0 ? NW * HT * QL * 64 : 1];
-  __shared__ int flag_sh[2][NW];  // per-wave "score above reference" flags, by stage parity
+  // per-wave "score above reference" flags, by stage parity; every lane stores the same
+  // value to its own word, which keeps the store out of divergent control flow
+  __shared__ int flag_sh[2][NW][64];
   uint8_t LDS_AS* smem = (uint8_t LDS_AS*)smem_raw;
 
   const int part = blockIdx.x;
@@ -343,7 +351,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
 
     // ---- query fragments (B operand of S^T = K Q^T), resident for the segment.  Rows
     // past the end re-load the last row; their results are never written.
-    i32x4 qf[HT][QR];
+    i32x4 qf[HT][kKSteps];
     int lim[HT];
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
@@ -358,11 +366,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
       for (int kk = 0; kk < kKSteps; ++kk) {
         // dims 8*sigma(kk, g) = 64*(kk/2) + 16*g + 8*(kk%2)
         const int d = 64 * (kk >> 1) + 8 * (kk & 1);
-        const i32x4 v = *(const i32x4*)(d < kRopeOff ? qn + d : qr + (d - kRopeOff));
-        if (kk < QR)
-          qf[ht][kk < QR ? kk : 0] = v;
-        else
-          qtail_sh[((wave * HT + ht) * (QL > 0 ? QL : 1) + (kk - QR)) * 64 + lane] = v;
+        qf[ht][kk] = *(const i32x4*)(d < kRopeOff ? qn + d : qr + (d - kRopeOff));
       }
     }
     const int lmin = L - (p.causal ? p.s_q - 1 : 0);  // every row sees tokens < lmin
@@ -375,8 +379,10 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
       // lane i holds the page id of page (first + i); ids are clamped into the pool
       pbase = first;
       if (paged) {
-        const int pi = pbase + lane;
-        int v = pi < np ? p.block_table[(int64_t)b * p.bt_stride + pi] : 0;
+        // branch-free: every lane loads an in-bounds entry (row b always has column 0)
+        const int last = np > 0 ? np - 1 : 0;
+        const int pi = pbase + lane < last ? pbase + lane : last;
+        const int v = p.block_table[(int64_t)b * p.bt_stride + pi];
         bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
       }
     };
@@ -434,7 +440,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
           if (k > 0) {
             int any = 0;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) any |= flag_sh[(k - 1) & 1][w];
+            for (int w = 0; w < NW; ++w) any |= flag_sh[(k - 1) & 1][w][0];
             if (any) {
               abort = true;
               break;
@@ -450,30 +456,26 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         // Fragment n = 2*kk + tt; DK fragments in flight ahead of the MFMAs.
         f32x4 acc[HT][2];
         i32x4 kf[DK];
-        i32x4 qt[HT][QL > 0 ? QL : 1];
+        // per-stage lane bases; the empty asm stops the compiler from precomputing one
+        // address register per fragment (the fragment offsets below fit the DS immediate)
+        const uint8_t LDS_AS* kb0 = sb + k_lane0;
+        const uint8_t LDS_AS* kb1 = sb + k_lane1;
+        asm volatile("" : "+v"(kb0));
+        asm volatile("" : "+v"(kb1));
 #define MLA_KFRAG(N) \
-  (*(const i32x4 LDS_AS*)(sb + (((N) >> 1) & 1 ? k_lane1 : k_lane0) + ((N) & 1) * kPanelBytes + ((N) >> 2) * 2048))
+  (*(const i32x4 LDS_AS*)((((N) >> 1) & 1 ? kb1 : kb0) + ((N) & 1) * kPanelBytes + ((N) >> 2) * 2048))
 #pragma unroll
         for (int n = 0; n < DK; ++n) kf[n] = MLA_KFRAG(n);
 #pragma unroll
         for (int n = 0; n < 2 * kKSteps; ++n) {
           const i32x4 a = kf[n % DK];
           if (n + DK < 2 * kKSteps) kf[n % DK] = MLA_KFRAG(n + DK);
-          if (QL > 0 && n == 2 * QR - DK) {  // query tail, DK fragments ahead of its use
-#pragma unroll
-            for (int ht = 0; ht < HT; ++ht)
-#pragma unroll
-              for (int j = 0; j < (QL > 0 ? QL : 1); ++j)
-                qt[ht][j] = qtail_sh[((wave * HT + ht) * (QL > 0 ? QL : 1) + j) * 64 + lane];
-          }
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) {
-            const int kk = n >> 1;
-            const i32x4 qb = kk < QR ? qf[ht][kk < QR ? kk : 0] : qt[ht][kk < QR ? 0 : kk - QR];
             if (n < 2)
-              mfma_qk_first<DT>(acc[ht][n & 1], a, qb);
+              mfma_qk_first<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
             else
-              mfma_qk<DT>(acc[ht][n & 1], a, qb);
+              mfma_qk<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -488,14 +490,18 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         // ---- mask tokens past each row's limit (sequence tail / causal)
         if (st * kStageTok + kStageTok > lmin) {
 #pragma unroll
-          for (int ht = 0; ht < HT; ++ht)
+          for (int ht = 0; ht < HT; ++ht) {
+            // token 16*tt + 4*g + r of the stage is visible iff 16*tt + r < rel; the empty
+            // asm keeps the compiler from hoisting one precomputed limit per (tt, r) out of
+            // the loop (that costs a register each)
+            int rel = lim[ht] - st * kStageTok - 4 * g;
+            asm volatile("" : "+v"(rel));
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const int t = st * kStageTok + 16 * tt + 4 * g + r;
-                if (t >= lim[ht]) acc[ht][tt][r] = -INFINITY;
-              }
+              for (int r = 0; r < 4; ++r)
+                if (16 * tt + r >= rel) acc[ht][tt][r] = -INFINITY;
+          }
         }
 
         // ---- this lane's largest scaled score per row tile
@@ -515,13 +521,13 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
           if (k == 0) {
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) m_ref[ht] = wave_max_g(lmx[ht]);
-            if (lane == 0) flag_sh[0][wave] = 0;
+            flag_sh[0][wave][lane] = 0;
           } else {
             bool over = false;
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
             const bool any = __builtin_amdgcn_ballot_w64(over) != 0;
-            if (lane == 0) flag_sh[k & 1][wave] = any ? 1 : 0;
+            flag_sh[k & 1][wave][lane] = any ? 1 : 0;
           }
         }
 
@@ -546,7 +552,9 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
 
         // ---- O^T += V^T P^T over the 32 tokens of the stage; DV fragments in flight
         i32x4 vf[DV];
-#define MLA_VFRAG(DTI) lds_tr_pair(sb + v_lane + (DTI) * 512)
+        const uint8_t LDS_AS* vb = sb + v_lane;
+        asm volatile("" : "+v"(vb));
+#define MLA_VFRAG(DTI) lds_tr_pair(vb + (DTI) * 512)
 #pragma unroll
         for (int n = 0; n < DV; ++n) vf[n] = MLA_VFRAG(n);
 #pragma unroll
@@ -558,6 +566,12 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
           __builtin_amdgcn_sched_barrier(0);
         }
 #undef MLA_VFRAG
+        // The last MFMAs are still reading their A/B operands (P^T and the last V^T fragment)
+        // over several passes after they issue.  The compiler's hazard model lets a VALU write
+        // reuse those registers a few cycles later (seen corrupting the last dim tile of the
+        // second row tile), so hold them for 32 wait states: the asm ties the operands, so no
+        // write to their registers can be placed before it.
+        operand_guard<HT>(pb, vf[(kDimTiles - 1) % DV]);
         if constexpr (MODE == kPassFirstStageRef) wait_lgkm0();  // flag store lands before the barrier
       }
       if constexpr (MODE == kPassFirstStageRef) {
@@ -565,7 +579,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
           lds_barrier();
           int any = 0;
 #pragma unroll
-          for (int w = 0; w < NW; ++w) any |= flag_sh[(nst - 1) & 1][w];
+          for (int w = 0; w < NW; ++w) any |= flag_sh[(nst - 1) & 1][w][0];
           abort = any != 0;
         }
       }
@@ -581,14 +595,20 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
       run_pass(std::integral_constant<int, kPassFixedRef>{});
     }
 
-    // ---- epilogue: finish the row sums, normalise, write final or partial output
+    // ---- epilogue: finish the row sums, normalise, write final or partial output.
+    // Branch-free on purpose (only uniform branches): at a divergent join the register
+    // allocator has placed the AGPR -> VGPR reload of an output tile in a block still running
+    // with a narrowed exec mask, so lanes outside it lost that tile.  Instead, lanes of
+    // padding rows (past the last row) store to the last row: their query was clamped to that
+    // row, so they computed bitwise the same values; and all four lane groups of a row store
+    // its lse (the same value).
     const int slot0 = p.splits[b];
     const bool single = (p.splits[b + 1] - slot0) == 1;
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
       const float l = wave_sum_g(l_part[ht]);
-      const int row = row0 + 16 * ht + li;
-      if (row >= p.rows) continue;
+      int row = row0 + 16 * ht + li;
+      row = row < p.rows ? row : p.rows - 1;
       const float inv = l > 0.f ? 1.f / l : 0.f;
       const float lse2 = l > 0.f ? m_ref[ht] + __log2f(l) : -INFINITY;
       const int s = row / p.heads;
@@ -601,8 +621,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
           *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (g == 0 && p.lse != nullptr)
-          p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
+        if (p.lse != nullptr) p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
       } else {
         const int64_t slot = slot0 + split;
         float* dst = p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
@@ -611,7 +630,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
           *(f32x4*)(dst + 16 * dt) = o[dt][ht] * inv;
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (g == 0) p.ws_lse[slot * p.rows + row] = lse2;
+        p.ws_lse[slot * p.rows + row] = lse2;
       }
     }
   }
@@ -716,12 +735,16 @@ struct Variant {
   int nw, ht, nstage;
 };
 
-// Rows per workgroup R = nw*16*ht; LDS per workgroup nstage*36 KiB.  A wave owns one 16-row
-// tile; above 64 rows the rows are split over ceil(rows/64) head blocks (grid dimension y).
+// Rows per workgroup R = nw*16*ht; LDS per workgroup nstage*36 KiB.  Up to 64 rows a wave
+// owns one 16-row tile (72 VGPRs of query, 128 AGPRs of fp32 output).  Above 64 rows a wave
+// owns two (32 rows: 144 VGPRs of query, 256 AGPRs of output), so one 128-row workgroup
+// reads each KV stage into LDS once for all its rows, and the K fragments it reads from LDS
+// serve twice the MFMA work; rows beyond 128 are split over ceil(rows/128) head blocks.
 Variant pick_variant(int rows) {
   if (rows <= 16) return {1, 1, 3};
   if (rows <= 32) return {2, 1, 3};
-  return {4, 1, 4};
+  if (rows <= 64) return {4, 1, 4};
+  return {4, 2, 3};
 }
 
 int wgs_per_cu(const Variant& v) {
@@ -761,7 +784,8 @@ template <int DT>
 hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blocks, hipStream_t st) {
   if (v.nw == 1) return launch_main<DT, 1, 1, 3>(kp, head_blocks, st);
   if (v.nw == 2) return launch_main<DT, 2, 1, 3>(kp, head_blocks, st);
-  return launch_main<DT, 4, 1, 4>(kp, head_blocks, st);
+  if (v.ht == 1) return launch_main<DT, 4, 1, 4>(kp, head_blocks, st);
+  return launch_main<DT, 4, 2, 3>(kp, head_blocks, st);
 }
 
 int validate(const mla_decode_args* a, int64_t* need_ws) {

@@ -84,10 +84,13 @@ def test_workspace_bytes(lib):
 
 
 def test_num_parts(lib):
-    # 16 / 32 / 64 rows -> one workgroup per CU; 128 rows -> two head blocks share a CU count
+    # one workgroup per CU; a workgroup covers up to 64 rows (<= 64 rows) or 128 rows (above),
+    # and the head blocks of a row set share the CU count
     assert lib.mla_num_parts(1, 1, 16, 1, 256) == 256
-    assert lib.mla_num_parts(64, 1, 128, 1, 256) == 128
-    assert lib.mla_num_parts(32, 2, 128, 1, 256) == 64
+    assert lib.mla_num_parts(1, 1, 64, 1, 256) == 256
+    assert lib.mla_num_parts(64, 1, 128, 1, 256) == 256
+    assert lib.mla_num_parts(32, 2, 128, 1, 256) == 128
+    assert lib.mla_num_parts(8, 1, 129, 1, 256) == 128
     assert lib.mla_num_parts(1, 1, 16, 2, 256) < 0
 
 
@@ -118,6 +121,8 @@ def _valid_args():
     ("batch", 0, 1, b"batch"),
     ("kv_nope", (1 << 20) + 8, 1, b"16-byte"),
     ("kv_stride_tok", 577, 1, b"strides"),
+    ("kv_stride_tok", 1 << 24, 4, b"2^24"),
+    ("kv_rope_stride_tok", 1 << 25, 4, b"2^24"),
     ("num_parts", 0, 1, b"num_parts"),
     ("sm_scale", 0.0, 1, b"sm_scale"),
     ("workspace_bytes", 0, 2, b"workspace"),
