@@ -33,6 +33,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline")
     ap.add_argument("--all-configs", action="store_true", help="also print one line per config to stderr")
+    ap.add_argument("--record", default="", metavar="PATH",
+                    help="with --all-configs: write the per-config record (tile, splits, timings, "
+                         "roofline) as JSON, the MI355X counterpart of mla_best_configs.json")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain MIB-MiB device copy 3x (scale for FETCH/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -172,14 +175,32 @@ def main():
     m = measure(args.config, args.steps, args.warmup)
     cfg = m["cfg"]
     if args.all_configs:
+        from mlc_decode_amd.api import kernel_variant
+        record = {"device": torch.cuda.get_device_name(0), "arch": "gfx950",
+                  "command": "python bench.py " + " ".join(sys.argv[1:]),
+                  "peaks": {"hbm_gbs": HBM_PEAK_GBS, "mfma_bf16_tflops": MFMA_PEAK_TFLOPS},
+                  "configs": {}}
         for name in ("C1", "C2", "C3", "C4", "C5"):
             mm = m if name == args.config else measure(name, max(20, args.steps // 4), 5)
-            print(json.dumps({"config": name, "us_call": round(mm["ms_call"] * 1e3, 2),
-                              "us_main": round(mm["ms_main"] * 1e3, 2),
-                              "us_combine": round(mm["ms_combine"] * 1e3, 2),
-                              "tbps": round(mm["gbs"] / 1e3, 3), "tflops": round(mm["tflops"], 1),
-                              "bound": mm["bound"], "parts": mm["parts"], "splits": mm["n_splits"]}),
-                  file=sys.stderr, flush=True)
+            c = mm["cfg"]
+            frac = (mm["gbs"] / HBM_PEAK_GBS) if mm["bound"] == "hbm" else (mm["tflops"] / MFMA_PEAK_TFLOPS)
+            entry = {"us_call": round(mm["ms_call"] * 1e3, 2), "us_main": round(mm["ms_main"] * 1e3, 2),
+                     "us_combine": round(mm["ms_combine"] * 1e3, 2),
+                     "us_metadata": round(mm["ms_meta"] * 1e3, 2),
+                     "tbps": round(mm["gbs"] / 1e3, 3), "tflops": round(mm["tflops"], 1),
+                     "bound": mm["bound"], "roofline_frac": round(frac, 4),
+                     "parts": mm["parts"], "splits": mm["n_splits"]}
+            print(json.dumps({"config": name, **entry}), file=sys.stderr, flush=True)
+            record["configs"][name] = {
+                "shape": {"batch": c.batch, "s_q": c.s_q, "heads": c.heads, "seqlen": c.seqlen,
+                          "dtype": "bf16" if c.dtype == torch.bfloat16 else "fp16",
+                          "causal": c.causal},
+                "splits_policy": f"forced {c.num_splits}" if c.num_splits else "balanced",
+                "tile": kernel_variant(c.s_q * c.heads), **entry}
+        if args.record:
+            with open(args.record, "w") as f:
+                json.dump(record, f, indent=1)
+                f.write("\n")
     peak = HBM_PEAK_GBS if m["bound"] == "hbm" else MFMA_PEAK_TFLOPS
     achieved = m["gbs"] if m["bound"] == "hbm" else m["tflops"]
     traffic = None

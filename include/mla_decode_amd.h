@@ -123,6 +123,15 @@ const char* mla_last_error(void);
 int mla_num_parts(int32_t batch, int32_t s_q, int32_t heads_q, int32_t heads_k, int32_t cu_count);
 
 /*
+ * Kernel tile chosen for `rows` = s_q * heads_q query rows: waves per workgroup, 16-row tiles
+ * per wave, LDS stages of 32 tokens in flight, rows per workgroup.  Returns 0, or
+ * MLA_ERR_INVALID for rows < 1 or a NULL output.  Replaces the block_H / threads / stages
+ * fields of the tuned-config record (mla_best_configs.json:1-73).
+ */
+int mla_variant(int32_t rows, int32_t* waves, int32_t* row_tiles, int32_t* stages,
+                int32_t* rows_per_workgroup);
+
+/*
  * Tile schedule on the device (one tiny kernel on `stream`).
  * cache_seqlens: [B] int32; tile_sched: [num_parts, 8] int32 out; num_splits: [B+1] int32 out.
  * forced_splits <= 0: balanced greedy packing over num_parts parts (every part gets about

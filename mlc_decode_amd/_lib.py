@@ -24,6 +24,7 @@ EXPORTED = (
     "mla_version",
     "mla_last_error",
     "mla_num_parts",
+    "mla_variant",
     "mla_get_metadata",
     "mla_get_metadata_host",
     "mla_workspace_bytes",
@@ -117,6 +118,8 @@ def load() -> ctypes.CDLL:
         lib.mla_last_error.restype = ctypes.c_char_p
         lib.mla_num_parts.argtypes = [_i32, _i32, _i32, _i32, _i32]
         lib.mla_num_parts.restype = ctypes.c_int
+        lib.mla_variant.argtypes = [_i32, _pi32, _pi32, _pi32, _pi32]
+        lib.mla_variant.restype = ctypes.c_int
         lib.mla_get_metadata.argtypes = [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]
         lib.mla_get_metadata.restype = ctypes.c_int
         lib.mla_get_metadata_host.argtypes = [_pi32, _i32, _i32, _i32, _i32, _pi32, _pi32]

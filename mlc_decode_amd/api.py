@@ -68,6 +68,15 @@ def num_parts_for(batch: int, s_q: int, heads_q: int, heads_k: int = 1, cu_count
     return n
 
 
+def kernel_variant(rows: int) -> dict:
+    """Tile of the main kernel for ``rows`` = s_q * heads query rows (``mla_variant``)."""
+    w, t, st, r = (ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32())
+    check("mla_variant", _lib.load().mla_variant(rows, ctypes.byref(w), ctypes.byref(t),
+                                                  ctypes.byref(st), ctypes.byref(r)))
+    return {"waves": w.value, "row_tiles_per_wave": t.value, "lds_stages": st.value,
+            "rows_per_workgroup": r.value, "stage_tokens": 32}
+
+
 def get_mla_metadata(cache_seqlens: torch.Tensor, num_heads_per_head_k: int, num_heads_k: int,
                      num_parts: Optional[int] = None, fixed_overhead: int = -1,
                      forced_splits: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:

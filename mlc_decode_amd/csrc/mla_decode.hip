@@ -294,7 +294,7 @@ __device__ __forceinline__ void wait_lgkm0() {
 
 template <int DT, int NW, int HT, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
-  static_assert((NSTAGE - 2) * (kLoadsPerStage / NW) < 64, "vmcnt would overflow");
+  static_assert((NSTAGE - 1) * (kLoadsPerStage / NW) < 64, "outstanding stage loads exceed vmcnt");
   static_assert(kLoadsPerStage % NW == 0, "loads per stage must split evenly");
   constexpr int R = NW * 16 * HT;
   constexpr int DK = 4;  // LDS prefetch depth of the QK A fragments
@@ -426,9 +426,22 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
       load_page_ids(page);
       wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
 
+      if constexpr (NSTAGE == 1) {
+        if (nst > 0) issue(0);
+      } else {
 #pragma unroll
-      for (int k = 0; k < NSTAGE - 1; ++k)
-        if (k < nst) issue(k);
+        for (int k = 0; k < NSTAGE - 1; ++k)
+          if (k < nst) issue(k);
+      }
+      // One LDS buffer (NSTAGE == 1): the next stage is loaded into it once every wave of
+      // the workgroup has consumed the current one; latency is hidden by the other
+      // workgroups sharing the CU instead.
+      auto refill_single = [&](int k) __attribute__((always_inline)) {
+        if constexpr (NSTAGE == 1) {
+          if constexpr (NW > 1) lds_barrier();
+          if (k + 1 < nst) issue(k + 1);
+        }
+      };
 
       bool abort = false;
 #pragma unroll 1
@@ -447,7 +460,9 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
             }
           }
         }
-        if (k + NSTAGE - 1 < nst) issue(k + NSTAGE - 1);
+        if constexpr (NSTAGE > 1) {
+          if (k + NSTAGE - 1 < nst) issue(k + NSTAGE - 1);
+        }
 
         const uint8_t LDS_AS* sb = smem + (k % NSTAGE) * kStageBytes;
         const int st = st_begin + k;
@@ -515,6 +530,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         if constexpr (MODE == kPassRowMax) {
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) m_ref[ht] = fmaxf(m_ref[ht], lmx[ht]);
+          refill_single(k);
           continue;
         }
         if constexpr (MODE == kPassFirstStageRef) {
@@ -572,6 +588,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         // second row tile), so hold them for 32 wait states: the asm ties the operands, so no
         // write to their registers can be placed before it.
         operand_guard<HT>(pb, vf[(kDimTiles - 1) % DV]);
+        refill_single(k);
         if constexpr (MODE == kPassFirstStageRef) wait_lgkm0();  // flag store lands before the barrier
       }
       if constexpr (MODE == kPassFirstStageRef) {
@@ -735,14 +752,18 @@ struct Variant {
   int nw, ht, nstage;
 };
 
-// Rows per workgroup R = nw*16*ht; LDS per workgroup nstage*36 KiB.  Up to 64 rows a wave
-// owns one 16-row tile (72 VGPRs of query, 128 AGPRs of fp32 output).  Above 64 rows a wave
-// owns two (32 rows: 144 VGPRs of query, 256 AGPRs of output), so one 128-row workgroup
-// reads each KV stage into LDS once for all its rows, and the K fragments it reads from LDS
-// serve twice the MFMA work; rows beyond 128 are split over ceil(rows/128) head blocks.
+// Rows per workgroup R = nw*16*ht; LDS per workgroup nstage*36 KiB.  A wave owns one 16-row
+// tile (72 VGPRs of query, 128 AGPRs of fp32 output) or two (32 rows: 144 VGPRs of query,
+// 256 AGPRs of output, and every K / V fragment read from LDS feeds two MFMAs).
+//  - up to 32 rows: one wave per workgroup with a single 36 KiB stage buffer, four
+//    workgroups per CU; each waits for its own stage while the others compute, which keeps
+//    4 x 36 KiB of loads in flight per CU (one wave alone could hold at most 63 KiB: vmcnt);
+//  - up to 64 rows: four waves of one tile sharing a 4-stage ring;
+//  - above 64 rows: four waves of two tiles (128 rows) sharing a 3-stage ring, so each KV
+//    stage is read into LDS once for all 128 rows; more rows use ceil(rows/128) head blocks.
 Variant pick_variant(int rows) {
-  if (rows <= 16) return {1, 1, 3};
-  if (rows <= 32) return {2, 1, 3};
+  if (rows <= 16) return {1, 1, 1};
+  if (rows <= 32) return {1, 2, 1};
   if (rows <= 64) return {4, 1, 4};
   return {4, 2, 3};
 }
@@ -782,8 +803,10 @@ hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) 
 
 template <int DT>
 hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blocks, hipStream_t st) {
-  if (v.nw == 1) return launch_main<DT, 1, 1, 3>(kp, head_blocks, st);
-  if (v.nw == 2) return launch_main<DT, 2, 1, 3>(kp, head_blocks, st);
+  if (v.nw == 1) {
+    if (v.ht == 1) return launch_main<DT, 1, 1, 1>(kp, head_blocks, st);
+    return launch_main<DT, 1, 2, 1>(kp, head_blocks, st);
+  }
   if (v.ht == 1) return launch_main<DT, 4, 1, 4>(kp, head_blocks, st);
   return launch_main<DT, 4, 2, 3>(kp, head_blocks, st);
 }
@@ -887,6 +910,18 @@ extern "C" {
 int mla_version(void) { return MLA_DECODE_AMD_VERSION; }
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
+
+int mla_variant(int32_t rows, int32_t* waves, int32_t* row_tiles, int32_t* stages,
+                int32_t* rows_per_workgroup) {
+  if (rows < 1 || !waves || !row_tiles || !stages || !rows_per_workgroup)
+    return fail(MLA_ERR_INVALID, "rows must be >= 1 and outputs non-NULL");
+  const Variant v = pick_variant(rows);
+  *waves = v.nw;
+  *row_tiles = v.ht;
+  *stages = v.nstage;
+  *rows_per_workgroup = v.nw * 16 * v.ht;
+  return MLA_OK;
+}
 
 int mla_num_parts(int32_t batch, int32_t s_q, int32_t heads_q, int32_t heads_k, int32_t cu_count) {
   if (batch < 1 || s_q < 1 || heads_q < 1 || heads_k != 1) {

@@ -84,14 +84,25 @@ def test_workspace_bytes(lib):
 
 
 def test_num_parts(lib):
-    # one workgroup per CU; a workgroup covers up to 64 rows (<= 64 rows) or 128 rows (above),
-    # and the head blocks of a row set share the CU count
-    assert lib.mla_num_parts(1, 1, 16, 1, 256) == 256
+    # up to 32 rows: four single-wave workgroups per CU; up to 64 rows: one 64-row workgroup
+    # per CU; above: one 128-row workgroup per CU, head blocks sharing the CU count
+    assert lib.mla_num_parts(1, 1, 16, 1, 256) == 1024
+    assert lib.mla_num_parts(1, 1, 32, 1, 256) == 1024
     assert lib.mla_num_parts(1, 1, 64, 1, 256) == 256
     assert lib.mla_num_parts(64, 1, 128, 1, 256) == 256
     assert lib.mla_num_parts(32, 2, 128, 1, 256) == 128
     assert lib.mla_num_parts(8, 1, 129, 1, 256) == 128
     assert lib.mla_num_parts(1, 1, 16, 2, 256) < 0
+
+
+def test_variant_query(lib):
+    vals = [ctypes.c_int32() for _ in range(4)]
+    ptrs = [ctypes.byref(v) for v in vals]
+    assert lib.mla_variant(16, *ptrs) == 0 and [v.value for v in vals] == [1, 1, 1, 16]
+    assert lib.mla_variant(32, *ptrs) == 0 and [v.value for v in vals] == [1, 2, 1, 32]
+    assert lib.mla_variant(64, *ptrs) == 0 and [v.value for v in vals] == [4, 1, 4, 64]
+    assert lib.mla_variant(128, *ptrs) == 0 and [v.value for v in vals] == [4, 2, 3, 128]
+    assert lib.mla_variant(0, *ptrs) == 1
 
 
 def _valid_args():

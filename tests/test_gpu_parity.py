@@ -129,6 +129,34 @@ def test_empty_sequence_and_nan_padding(gpu):
     assert torch.all(out[~good].float() == 0) and torch.all(lse[~good].cpu() == -math.inf)
 
 
+@pytest.mark.parametrize("H", [16, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_reference_fallback_pass(gpu, H, dtype):
+    """Scores far above the first stage's row max force the exact two-pass redo of a segment.
+
+    The rope dims of every token past the first 32 of a sequence are scaled by 100: the
+    scaled scores then spread by ~30 natural-log units (far more than the reference margin of
+    64 / 15 log2 units for bf16 / fp16).  Such softmaxes are dominated by single tokens, so
+    out ~ one V row; the latent dims (V) are scaled by 1/4 to keep |out| < 2, where the bf16
+    rounding of the output itself stays below 0.004 (at |out| >= 4 half a bf16 ulp alone is
+    0.0156, beyond the 1e-2 bar for any bf16 output)."""
+    lengths = [200, 64, 1000, 33]
+    cfg = small_cfg(f"fallback_h{H}", len(lengths), 1, H, lengths, dtype)
+    inp = make_inputs(cfg, seed=21)
+    inp.kv_cache[..., :512] *= 0.25
+    for b, L in enumerate(lengths):
+        t = torch.arange(32, L)
+        pages = inp.block_table[b, t // 64].long()
+        inp.kv_cache[pages, t % 64, 0, 512:] *= 100
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                  inp.sm_scale, True)
+    assert ref_l.max() - ref_l.min() > 20  # the scores really did spread
+    for ns in (None, 1, 3):
+        say(f"fallback H={H} dtype={dtype} num_splits={ns}")
+        out, lse = run_paged(inp, gpu, ns)
+        assert_parity(out, lse, ref_o, ref_l, f"fallback H={H} ns={ns}")
+
+
 def test_golden_fixtures_on_gpu(gpu):
     import numpy as np
     from test_oracle import GOLDEN, load_case

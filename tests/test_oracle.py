@@ -212,10 +212,22 @@ def test_forced_schedule_bruteforce():
 
 
 def test_oracle_mistakes_are_caught():
-    """A planted mistake in the oracle (dropping the rope dims) fails the fixture check."""
+    """Planted mistakes in the oracle (dropping the rope dims, a wrong scale, a reversed page
+    walk) each fail the fixture check."""
     z = np.load(GOLDEN)
     c = load_case(z, "h16_tails")
     q = c["q"].clone()
     q[..., 512:] = 0  # what an oracle that forgot q_rope . k_rope would compute
     out, _ = R.decode_paged(q, c["kv"], c["table"], c["lengths"], SCALE, c["causal"])
+    assert not torch.allclose(out, c["out"], atol=2e-5, rtol=1e-4)
+    # a wrong softmax scale (the 512-d latent width instead of 576)
+    out, lse = R.decode_paged(c["q"], c["kv"], c["table"], c["lengths"], 512 ** -0.5, c["causal"])
+    assert not torch.allclose(out, c["out"], atol=2e-5, rtol=1e-4)
+    # a transposed page walk: the pages of each sequence visited in reverse order
+    table = c["table"].clone()
+    for b, L in enumerate(c["lengths"].tolist()):
+        n = R.pages_of(L)
+        if n > 1:
+            table[b, :n] = table[b, :n].flip(0)
+    out, _ = R.decode_paged(c["q"], c["kv"], table, c["lengths"], SCALE, c["causal"])
     assert not torch.allclose(out, c["out"], atol=2e-5, rtol=1e-4)
