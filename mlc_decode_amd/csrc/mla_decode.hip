@@ -294,8 +294,11 @@ __device__ __forceinline__ void wait_lgkm0() {
 
 template <int DT, int NW, int HT, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
-  static_assert((NSTAGE - 1) * (kLoadsPerStage / NW) < 64, "outstanding stage loads exceed vmcnt");
-  static_assert(kLoadsPerStage % NW == 0, "loads per stage must split evenly");
+  // Stage loads are issued by the first NL waves (all of them up to four); with eight waves
+  // the other four only consume, and the per-stage barrier orders them after the loads.
+  constexpr int NL = NW < 4 ? NW : 4;
+  static_assert((NSTAGE - 1) * (kLoadsPerStage / NL) < 64, "outstanding stage loads exceed vmcnt");
+  static_assert(kLoadsPerStage % NL == 0, "loads per stage must split evenly");
   constexpr int R = NW * 16 * HT;
   constexpr int DK = 4;  // LDS prefetch depth of the QK A fragments
   constexpr int DV = 4;  // LDS prefetch depth of the PV A fragments
@@ -403,8 +406,9 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         rb = p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st);
       }
       const int left = L - st * kStageTok;
-      issue_stage<NW>(smem + (k % NSTAGE) * kStageBytes, nb, rb, kv_st, kr_st,
-                      (left < kStageTok ? left : kStageTok) - 1, wave, lane);
+      if (wave < NL)  // uniform
+        issue_stage<NL>(smem + (k % NSTAGE) * kStageBytes, nb, rb, kv_st, kr_st,
+                        (left < kStageTok ? left : kStageTok) - 1, wave, lane);
     };
 
     // One pass over the segment's stages.  Returns true (uniformly across the workgroup)
@@ -447,7 +451,8 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
 #pragma unroll 1
       for (int k = 0; k < nst; ++k) {
         const int remaining_after = nst - 1 - k;
-        wait_stage<NW, NSTAGE>(remaining_after < NSTAGE - 2 ? remaining_after : NSTAGE - 2);
+        if (wave < NL)  // uniform
+          wait_stage<NL, NSTAGE>(remaining_after < NSTAGE - 2 ? remaining_after : NSTAGE - 2);
         lds_barrier();
         if constexpr (MODE == kPassFirstStageRef) {
           if (k > 0) {
