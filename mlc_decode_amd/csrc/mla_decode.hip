@@ -142,17 +142,26 @@ __device__ __forceinline__ void operand_guard(i32x4 (&pb)[HT], i32x4& va) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(pb[0]), "+v"(va));
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to nearest even and packed low-first: one v_cvt_pk_{bf16,f16}_f32.
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  if constexpr (DT == MLA_DTYPE_BF16) {
-    const __bf16 x = (__bf16)a, y = (__bf16)b;  // round to nearest even
-    return (uint32_t)__builtin_bit_cast(uint16_t, x) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
-  } else {
-    const _Float16 x = (_Float16)a, y = (_Float16)b;
-    return (uint32_t)__builtin_bit_cast(uint16_t, x) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
-  }
+  const f32x2 v = {a, b};
+  if constexpr (DT == MLA_DTYPE_BF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// max of three floats in one v_max3_f32 (fmaxf would first canonicalise each operand for
+// signalling-NaN semantics; scores here are finite or -inf)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
 }
 
 template <int DT>
@@ -292,21 +301,40 @@ __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
 
+// Waves per SIMD a variant is compiled for: one 16-row tile per wave with at most a 2-stage
+// ring fits 256 registers, so two workgroups (or eight waves) share a CU; everything else
+// takes the whole register file (one wave per SIMD).
+constexpr int waves_per_simd(int nw, int ht, int nstage) {
+  return (ht == 1 && (nw == 8 || (nw == 4 && nstage <= 2))) ? 2 : 1;
+}
+
 template <int DT, int NW, int HT, int NSTAGE>
-__global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
+__global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE) * 4 / NW > 0
+                                          ? waves_per_simd(NW, HT, NSTAGE) * 4 / NW : 1)
+void mla_splitkv_kernel(KParams p) {
   // Stage loads are issued by the first NL waves (all of them up to four); with eight waves
   // the other four only consume, and the per-stage barrier orders them after the loads.
   constexpr int NL = NW < 4 ? NW : 4;
+  // With eight waves the second four run half a stage behind: each iteration they finish the
+  // previous stage's PV and then do this stage's QK, so on every SIMD one wave is reading K
+  // and issuing QK MFMAs while the other reads V^T for PV.  A lagging group still reads the
+  // previous stage's slot, so loads run LEAD = NSTAGE - 2 stages ahead instead of NSTAGE - 1.
+  constexpr bool kSkew = NW == 8;
+  constexpr int LEAD = kSkew ? NSTAGE - 2 : NSTAGE - 1;
+  static_assert(!kSkew || NSTAGE >= 3, "the skewed layout needs a ring of at least 3 stages");
   static_assert((NSTAGE - 1) * (kLoadsPerStage / NL) < 64, "outstanding stage loads exceed vmcnt");
   static_assert(kLoadsPerStage % NL == 0, "loads per stage must split evenly");
   constexpr int R = NW * 16 * HT;
   constexpr int DK = 4;  // LDS prefetch depth of the QK A fragments
-  constexpr int DV = 4;  // LDS prefetch depth of the PV A fragments
+  constexpr int DV = HT == 2 ? 2 : 4;  // LDS prefetch depth of the PV A fragments
   constexpr float kTau = ref_tau<DT>();
   __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[NSTAGE * kStageBytes];
-  // per-wave "score above reference" flags, by stage parity; every lane stores the same
-  // value to its own word, which keeps the store out of divergent control flow
-  __shared__ int flag_sh[2][NW][64];
+  // "score above reference" words, one per stage modulo 4.  A wave whose stage-k scores exceed
+  // the reference stores 1 into over_sh[k % 4] (a wave-uniform branch, all lanes storing the
+  // same value); every wave reads the word after the next barrier; wave 0 clears it two
+  // stages later, once every wave has read it, and two barriers separate that clear from the
+  // word's next use.
+  __shared__ int over_sh[4];
   uint8_t LDS_AS* smem = (uint8_t LDS_AS*)smem_raw;
 
   const int part = blockIdx.x;
@@ -427,6 +455,10 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) m_ref[ht] = -INFINITY;
       }
+      if constexpr (MODE == kPassFirstStageRef) {
+        if (wave == 0) over_sh[lane & 3] = 0;  // uniform branch; ordered by the first barriers
+        wait_lgkm0();
+      }
       load_page_ids(page);
       wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
 
@@ -434,7 +466,7 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         if (nst > 0) issue(0);
       } else {
 #pragma unroll
-        for (int k = 0; k < NSTAGE - 1; ++k)
+        for (int k = 0; k < LEAD; ++k)
           if (k < nst) issue(k);
       }
       // One LDS buffer (NSTAGE == 1): the next stage is loaded into it once every wave of
@@ -447,30 +479,66 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         }
       };
 
+      // ---- O^T += V^T P^T over the 32 tokens of stage kp; DV fragments in flight
+      auto v_base = [&](int kp) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* vb = smem + (kp % NSTAGE) * kStageBytes + v_lane;
+        asm volatile("" : "+v"(vb));
+        return vb;
+      };
+      // the first DV V^T fragments of stage kp (issued ahead of the softmax to hide latency)
+      auto v_prefetch = [&](int kp, i32x4 (&vf)[DV]) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* vb = v_base(kp);
+#pragma unroll
+        for (int n = 0; n < DV; ++n) vf[n] = lds_tr_pair(vb + n * 512);
+      };
+      auto pv_stage = [&](int kp, i32x4 (&pb)[HT], i32x4 (&vf)[DV]) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* vb = v_base(kp);
+#define MLA_VFRAG(DTI) lds_tr_pair(vb + (DTI) * 512)
+#pragma unroll
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          const i32x4 a = vf[dt % DV];
+          if (dt + DV < kDimTiles) vf[dt % DV] = MLA_VFRAG(dt + DV);
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) o[dt][ht] = mfma32<DT>(a, pb[ht], o[dt][ht]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#undef MLA_VFRAG
+        // The last MFMAs are still reading their A/B operands (P^T and the last V^T fragment)
+        // over several passes after they issue.  The compiler's hazard model lets a VALU write
+        // reuse those registers a few cycles later (seen corrupting the last dim tile of the
+        // second row tile), so hold them for 32 wait states: the asm ties the operands, so no
+        // write to their registers can be placed before it.
+        operand_guard<HT>(pb, vf[(kDimTiles - 1) % DV]);
+      };
+      const bool lagging = kSkew && wave >= NW / 2;  // uniform
+      i32x4 pb_lag[HT];
+
       bool abort = false;
 #pragma unroll 1
       for (int k = 0; k < nst; ++k) {
         const int remaining_after = nst - 1 - k;
         if (wave < NL)  // uniform
-          wait_stage<NL, NSTAGE>(remaining_after < NSTAGE - 2 ? remaining_after : NSTAGE - 2);
+          wait_stage<NL, NSTAGE>(remaining_after < LEAD - 1 ? remaining_after : LEAD - 1);
         lds_barrier();
+        // the previous stage's flags, read now and tested after this stage's QK product
+        int prev_over = 0;
         if constexpr (MODE == kPassFirstStageRef) {
-          if (k > 0) {
-            int any = 0;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) any |= flag_sh[(k - 1) & 1][w][0];
-            if (any) {
-              abort = true;
-              break;
-            }
-          }
+          if (k > 0) prev_over = over_sh[(k - 1) & 3];
+          if (k > 1 && wave == 0) over_sh[(k - 2) & 3] = 0;  // uniform branch
         }
         if constexpr (NSTAGE > 1) {
-          if (k + NSTAGE - 1 < nst) issue(k + NSTAGE - 1);
+          if (k + LEAD < nst) issue(k + LEAD);
         }
 
         const uint8_t LDS_AS* sb = smem + (k % NSTAGE) * kStageBytes;
         const int st = st_begin + k;
+        if constexpr (kSkew && MODE != kPassRowMax) {
+          if (lagging && k > 0) {
+            i32x4 vfl[DV];
+            v_prefetch(k - 1, vfl);
+            pv_stage(k - 1, pb_lag, vfl);
+          }
+        }
 
         // ---- S^T = K Q^T over 576 dims: two 16-token tiles x HT 16-row tiles.
         // Fragment n = 2*kk + tt; DK fragments in flight ahead of the MFMAs.
@@ -506,6 +574,16 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
           if (ht > 0) qk_touch(acc[ht][0]);
           qk_touch(acc[ht][1]);
         }
+        if constexpr (MODE == kPassFirstStageRef) {
+          if (prev_over) {  // uniform: every wave read the same flags after the same barrier
+            abort = true;
+            break;
+          }
+        }
+        i32x4 vf[DV];
+        if constexpr (MODE != kPassRowMax) {
+          if (!(kSkew && lagging)) v_prefetch(k, vf);
+        }
 
         // ---- mask tokens past each row's limit (sequence tail / causal)
         if (st * kStageTok + kStageTok > lmin) {
@@ -528,8 +606,9 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         float lmx[HT];
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) {
-          const float v = fmaxf(fmaxf(fmaxf(acc[ht][0][0], acc[ht][0][1]), fmaxf(acc[ht][0][2], acc[ht][0][3])),
-                                fmaxf(fmaxf(acc[ht][1][0], acc[ht][1][1]), fmaxf(acc[ht][1][2], acc[ht][1][3])));
+          const float v = max3f(max3f(acc[ht][0][0], acc[ht][0][1], acc[ht][0][2]),
+                                max3f(acc[ht][0][3], acc[ht][1][0], acc[ht][1][1]),
+                                max3f(acc[ht][1][2], acc[ht][1][3], -INFINITY));
           lmx[ht] = v * p.scale_log2;
         }
         if constexpr (MODE == kPassRowMax) {
@@ -542,13 +621,11 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
           if (k == 0) {
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) m_ref[ht] = wave_max_g(lmx[ht]);
-            flag_sh[0][wave][lane] = 0;
           } else {
             bool over = false;
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
-            const bool any = __builtin_amdgcn_ballot_w64(over) != 0;
-            flag_sh[k & 1][wave][lane] = any ? 1 : 0;
+            if (__builtin_amdgcn_ballot_w64(over) != 0) over_sh[k & 3] = 1;  // uniform branch
           }
         }
 
@@ -558,51 +635,40 @@ __global__ __launch_bounds__(NW * 64, 1) void mla_splitkv_kernel(KParams p) {
         for (int ht = 0; ht < HT; ++ht) {
           const float mu = m_ref[ht] == -INFINITY ? 0.f : m_ref[ht];
           float pv[2][4];
-          float sum = 0.f;
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
-              sum += pv[tt][r];
-            }
-          l_part[ht] += sum;
+            for (int r = 0; r < 4; ++r) pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
+          l_part[ht] += ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) +
+                        ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3]));
           pb[ht] = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
                          (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
         }
 
-        // ---- O^T += V^T P^T over the 32 tokens of the stage; DV fragments in flight
-        i32x4 vf[DV];
-        const uint8_t LDS_AS* vb = sb + v_lane;
-        asm volatile("" : "+v"(vb));
-#define MLA_VFRAG(DTI) lds_tr_pair(vb + (DTI) * 512)
+        if constexpr (kSkew) {
+          if (lagging) {
 #pragma unroll
-        for (int n = 0; n < DV; ++n) vf[n] = MLA_VFRAG(n);
-#pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) {
-          const i32x4 a = vf[dt % DV];
-          if (dt + DV < kDimTiles) vf[dt % DV] = MLA_VFRAG(dt + DV);
-#pragma unroll
-          for (int ht = 0; ht < HT; ++ht) o[dt][ht] = mfma32<DT>(a, pb[ht], o[dt][ht]);
-          __builtin_amdgcn_sched_barrier(0);
+            for (int ht = 0; ht < HT; ++ht) pb_lag[ht] = pb[ht];
+          } else {
+            pv_stage(k, pb, vf);
+          }
+        } else {
+          pv_stage(k, pb, vf);
         }
-#undef MLA_VFRAG
-        // The last MFMAs are still reading their A/B operands (P^T and the last V^T fragment)
-        // over several passes after they issue.  The compiler's hazard model lets a VALU write
-        // reuse those registers a few cycles later (seen corrupting the last dim tile of the
-        // second row tile), so hold them for 32 wait states: the asm ties the operands, so no
-        // write to their registers can be placed before it.
-        operand_guard<HT>(pb, vf[(kDimTiles - 1) % DV]);
         refill_single(k);
         if constexpr (MODE == kPassFirstStageRef) wait_lgkm0();  // flag store lands before the barrier
+      }
+      if constexpr (kSkew && MODE != kPassRowMax) {
+        if (lagging && !abort && nst > 0) {
+          i32x4 vfl[DV];
+          v_prefetch(nst - 1, vfl);
+          pv_stage(nst - 1, pb_lag, vfl);
+        }
       }
       if constexpr (MODE == kPassFirstStageRef) {
         if (!abort && nst > 1) {  // the last stage's flags
           lds_barrier();
-          int any = 0;
-#pragma unroll
-          for (int w = 0; w < NW; ++w) any |= flag_sh[(nst - 1) & 1][w][0];
-          abort = any != 0;
+          abort = over_sh[(nst - 1) & 3] != 0;
         }
       }
       wait_vmcnt<0>();  // an abandoned pass may leave stage loads in flight
@@ -777,7 +843,8 @@ int wgs_per_cu(const Variant& v) {
   const int lds = v.nstage * mla::kStageBytes;
   int by_lds = (160 * 1024) / lds;
   if (by_lds < 1) by_lds = 1;
-  const int by_waves = 4 / v.nw > 0 ? 4 / v.nw : 1;  // one wave per SIMD at full register use
+  const int per_simd = mla::waves_per_simd(v.nw, v.ht, v.nstage);
+  const int by_waves = 4 * per_simd / v.nw > 0 ? 4 * per_simd / v.nw : 1;
   return by_lds < by_waves ? by_lds : by_waves;
 }
 
