@@ -175,6 +175,7 @@ def main():
     m = measure(args.config, args.steps, args.warmup)
     cfg = m["cfg"]
     if args.all_configs:
+        from mlc_decode_amd import _lib
         from mlc_decode_amd.api import kernel_variant
         record = {"device": torch.cuda.get_device_name(0), "arch": "gfx950",
                   "command": "python bench.py " + " ".join(sys.argv[1:]),
@@ -195,7 +196,8 @@ def main():
                 "shape": {"batch": c.batch, "s_q": c.s_q, "heads": c.heads, "seqlen": c.seqlen,
                           "dtype": "bf16" if c.dtype == torch.bfloat16 else "fp16",
                           "causal": c.causal},
-                "splits_policy": f"forced {c.num_splits}" if c.num_splits else "balanced",
+                "splits_policy": (f"forced {c.num_splits}" if c.num_splits
+                                  else f"min-payload, overhead {_lib.MLA_DEFAULT_SPLIT_OVERHEAD} pages"),
                 "tile": kernel_variant(c.s_q * c.heads), **entry}
         if args.record:
             with open(args.record, "w") as f:

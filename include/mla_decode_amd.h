@@ -52,6 +52,8 @@ extern "C" {
 #define MLA_PAGE_TOKENS 64
 /* Each part of the tile schedule is described by this many int32 words. */
 #define MLA_SCHED_WORDS 8
+/* Per-split overhead, in pages, of the default (min-payload) tile schedule. */
+#define MLA_DEFAULT_SPLIT_OVERHEAD 2
 
 /*
  * Decode arguments.  Strides are in elements.  The latent ("nope", dims
@@ -134,9 +136,13 @@ int mla_variant(int32_t rows, int32_t* waves, int32_t* row_tiles, int32_t* stage
 /*
  * Tile schedule on the device (one tiny kernel on `stream`).
  * cache_seqlens: [B] int32; tile_sched: [num_parts, 8] int32 out; num_splits: [B+1] int32 out.
- * forced_splits <= 0: balanced greedy packing over num_parts parts (every part gets about
- *   total/num_parts 64-token pages plus a fixed per-split overhead of fixed_overhead pages;
- *   fixed_overhead < 0 selects the built-in default).
+ * forced_splits <= 0: greedy packing over num_parts parts in (sequence, page) order, a split
+ *   costing its 64-token pages plus a per-split overhead of f pages, up to a payload per part:
+ *   fixed_overhead >= 0: f = fixed_overhead and the reference's payload
+ *     ceil(total / num_parts) + f, total = sum of (pages + f) (FlashMLA's rule);
+ *   fixed_overhead < 0: f = MLA_DEFAULT_SPLIT_OVERHEAD and the smallest payload in
+ *     [ceil(total / num_parts), ceil(total / num_parts) + f] whose packing fits num_parts parts
+ *     (the default: the shortest critical part the greedy rule allows).
  * forced_splits > 0: every sequence is cut into min(forced_splits, pages) contiguous
  *   near-equal page ranges (the spread family of mla_decode.py:9-30); then
  *   num_parts must equal batch * forced_splits.
@@ -151,7 +157,12 @@ int mla_get_metadata_host(const int32_t* cache_seqlens, int32_t batch, int32_t n
                           int32_t fixed_overhead, int32_t forced_splits, int32_t* tile_sched,
                           int32_t* num_splits);
 
-/* Workspace bytes mla_decode_fwd needs for this problem and part count. */
+/*
+ * Workspace bytes mla_decode_fwd needs for this problem and part count: the per-split
+ * log2-domain lse [slots, rows] fp32 (padded to 256 bytes), then the per-split
+ * softmax-normalised partial outputs [slots, rows, 512] in the input dtype (16-bit, as the
+ * reference's output_partial, mla_decode.py:73-74), with slots = batch + num_parts.
+ */
 int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t num_parts);
 
 /*

@@ -83,9 +83,12 @@ def get_mla_metadata(cache_seqlens: torch.Tensor, num_heads_per_head_k: int, num
     """Tile schedule: ``(tile_scheduler_metadata [num_parts, 8] int32, num_splits [B+1] int32)``.
 
     ``num_heads_per_head_k`` is ``s_q * h_q // h_kv`` as in the reference's call; it picks
-    the kernel's row blocking and hence the part count.  ``forced_splits > 0`` cuts every
-    sequence into that many near-equal page ranges instead of balancing (then
-    ``num_parts = B * forced_splits``).
+    the kernel's row blocking and hence the part count.  Parts are packed greedily with a
+    per-split overhead of ``fixed_overhead`` pages at the reference's payload
+    ``ceil(total / parts) + fixed_overhead``; the default (``fixed_overhead < 0``) packs at the
+    smallest payload that fits, with the library's overhead ``MLA_DEFAULT_SPLIT_OVERHEAD``.
+    ``forced_splits > 0`` cuts every sequence into that many near-equal page ranges instead
+    (then ``num_parts = B * forced_splits``).
     """
     _require_gpu(cache_seqlens, "cache_seqlens")
     if num_heads_k != 1:

@@ -33,6 +33,7 @@
 #include <mutex>
 #include <string>
 #include <type_traits>
+#include <vector>
 
 #include "mla_decode_amd.h"
 #include "mla_sched.h"
@@ -79,8 +80,8 @@ struct KParams {
   uint16_t* out;
   int64_t o_sb, o_ss, o_sh;
   float* lse;
-  float* ws_lse;  // [slots, rows] log2-domain lse of each split
-  float* ws_o;    // [slots, rows, 512] softmax-normalised partial outputs
+  float* ws_lse;    // [slots, rows] log2-domain lse of each split
+  uint16_t* ws_o;   // [slots, rows, 512] softmax-normalised partial outputs, input dtype
   int32_t batch, s_q, heads, rows, causal, num_parts;
   float scale_log2;  // sm_scale * log2(e)
 };
@@ -179,8 +180,12 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // lane l reads base + voff_l and its 16 bytes land at LDS byte lds_addr + 16*l.  Issued as
 // inline asm on purpose: the compiler then does not track it as an LDS store, so it adds no
 // conservative vmcnt(0) waits before the LDS reads of *other* stages; completion is awaited
-// explicitly (wait_stage) before a barrier.  M0 (the LDS base of the copy) is saved and
-// restored around it.
+// explicitly (wait_stage) before a barrier.  M0 (the LDS base of the copy) is written without
+// a save/restore: M0 is a reserved register, which clang does not preserve for a clobber, and
+// nothing else in these kernels reads it (no LDS-DMA builtins, message sends or relative
+// register moves; the generated code has no M0 reader besides these copies).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds_addr) {
   // base and lds_addr are uniform; readfirstlane makes that visible to the register allocator.
   // The builtin returns a signed int: each half goes through uint32_t before widening, or a
@@ -189,16 +194,14 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b64);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b64 >> 32));
   const uint64_t sbase = ((uint64_t)hi << 32) | (uint64_t)lo;
-  uint32_t saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "global_load_lds_dwordx4 %1, %2\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
       : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-      : "memory");
+      : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Workgroup barrier for LDS hand-off only.  Each wave has already waited for its own DMA
 // copies (vmcnt) and consumed its own LDS reads, so no memory-model fence is needed (the
@@ -701,23 +704,21 @@ void mla_splitkv_kernel(KParams p) {
       const float lse2 = l > 0.f ? m_ref[ht] + __log2f(l) : -INFINITY;
       const int s = row / p.heads;
       const int h = row - s * p.heads;
-      if (single) {
-        uint16_t* dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 4 * g;
+      // A single-split sequence writes its output directly; otherwise the split's partial goes
+      // to the workspace in the input dtype (the split partials of the reference's kernel,
+      // mla_decode.py:73-74,192, are in the input dtype too).
+      const int64_t slot = slot0 + split;
+      uint16_t* dst = single ? p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 4 * g
+                             : p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
 #pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) {  // one tile at a time (register pressure)
-          const f32x4 v = o[dt][ht] * inv;
-          *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
-          __builtin_amdgcn_sched_barrier(0);
-        }
+      for (int dt = 0; dt < kDimTiles; ++dt) {  // one tile at a time (register pressure)
+        const f32x4 v = o[dt][ht] * inv;
+        *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (single) {
         if (p.lse != nullptr) p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
       } else {
-        const int64_t slot = slot0 + split;
-        float* dst = p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
-#pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) {
-          *(f32x4*)(dst + 16 * dt) = o[dt][ht] * inv;
-          __builtin_amdgcn_sched_barrier(0);
-        }
         p.ws_lse[slot * p.rows + row] = lse2;
       }
     }
@@ -727,8 +728,39 @@ void mla_splitkv_kernel(KParams p) {
 // ---------------------------------------------------------------------------------------
 // combine: LSE-weighted merge of the splits of each (sequence, row)
 // ---------------------------------------------------------------------------------------
+// Eight consecutive partial values of one row, widened to fp32: from the fp32 partials of
+// mla_merge_partials or from the 16-bit (input dtype) partials of the decode workspace.
 template <int DT>
-__global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restrict__ ws_o,
+__device__ __forceinline__ void load8(const float* src, float (&x)[8]) {
+  const f32x4 a = *(const f32x4*)src;
+  const f32x4 c = *(const f32x4*)(src + 4);
+  x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+  x[4] = c[0]; x[5] = c[1]; x[6] = c[2]; x[7] = c[3];
+}
+template <int DT>
+__device__ __forceinline__ void load8(const uint16_t* src, float (&x)[8]) {
+  const i32x4 v = *(const i32x4*)src;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (DT == MLA_DTYPE_BF16) {
+      x[2 * j] = __builtin_bit_cast(float, (uint32_t)v[j] << 16);
+      x[2 * j + 1] = __builtin_bit_cast(float, (uint32_t)v[j] & 0xffff0000u);
+    } else {
+      // copied to a scalar first: __builtin_bit_cast applied to the vector element itself
+      // compiled to a read of element 0 for every j
+      const int w = v[j];
+      const f16x2 h = __builtin_bit_cast(f16x2, w);
+      x[2 * j] = (float)h[0];
+      x[2 * j + 1] = (float)h[1];
+    }
+  }
+}
+
+// One wave per (sequence, row); lane l owns output columns 8l .. 8l+7.  Split weights are
+// exp2(lse_k - lse) with lse the log2-sum-exp2 over the row's splits, staged through LDS so
+// every lane reads them; the partial rows are read four splits at a time (independent loads).
+template <int DT, typename PT>
+__global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__ ws_o,
                                                           const float* __restrict__ ws_lse,
                                                           const int32_t* __restrict__ splits,
                                                           int rows, int heads, int s_q,
@@ -760,6 +792,8 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  const PT* src0 = ws_o + ((int64_t)base * rows + row) * kDV + lane * 8;
+  const int64_t split_stride = (int64_t)rows * kDV;
   for (int k0 = 0; k0 < n; k0 += 64) {
     const int k = k0 + lane;
     float w = 0.f;
@@ -767,13 +801,24 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
     w_sh[wave][lane] = w;
     __builtin_amdgcn_wave_barrier();
     const int kn = n - k0 < 64 ? n - k0 : 64;
-    for (int kk = 0; kk < kn; ++kk) {
+    int kk = 0;
+    for (; kk + 4 <= kn; kk += 4) {
+      float x[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load8<DT>(src0 + (k0 + kk + u) * split_stride, x[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wk = w_sh[wave][kk + u];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += wk * x[u][j];
+      }
+    }
+    for (; kk < kn; ++kk) {
+      float x[8];
+      load8<DT>(src0 + (k0 + kk) * split_stride, x);
       const float wk = w_sh[wave][kk];
-      const float* src = ws_o + ((int64_t)(base + k0 + kk) * rows + row) * kDV + lane * 8;
-      const f32x4 x0 = *(const f32x4*)src;
-      const f32x4 x1 = *(const f32x4*)(src + 4);
-      acc[0] += wk * x0[0]; acc[1] += wk * x0[1]; acc[2] += wk * x0[2]; acc[3] += wk * x0[3];
-      acc[4] += wk * x1[0]; acc[5] += wk * x1[1]; acc[6] += wk * x1[2]; acc[7] += wk * x1[3];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += wk * x[j];
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -786,23 +831,107 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const float* __restric
 }
 
 // ---------------------------------------------------------------------------------------
-// tile schedule on the device: lengths staged in LDS, then one thread packs the parts
+// tile schedule on the device: one workgroup.  Pages staged in LDS and summed; each candidate
+// payload is tested by one thread (a serial pass over the sequences with the closed-form
+// packing step), which also records the packing state at the start of each of 256 sequence
+// chunks; then every thread replays its own chunk from that state and writes the records of
+// the parts that begin in it, so the records are written in parallel.  Produces exactly the
+// host schedule (same packing functions).
 // ---------------------------------------------------------------------------------------
 constexpr int kMetaMaxBatch = 16384;
+constexpr int kMetaThreads = 256;
+constexpr int kMetaMaxCand = 8;
 
-__global__ __launch_bounds__(256) void mla_metadata_kernel(const int32_t* __restrict__ seqlens,
-                                                           int batch, int num_parts,
-                                                           int fixed_overhead, int forced,
-                                                           int32_t* __restrict__ sched,
-                                                           int32_t* __restrict__ splits) {
-  __shared__ int32_t len_sh[kMetaMaxBatch];
-  for (int i = threadIdx.x; i < batch; i += blockDim.x) len_sh[i] = seqlens[i];
+__global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
+    const int32_t* __restrict__ seqlens, int batch, int num_parts, int f, int min_payload,
+    int forced, int32_t* __restrict__ sched, int32_t* __restrict__ splits) {
+  __shared__ int32_t pg_sh[kMetaMaxBatch];
+  __shared__ PackState st_sh[kMetaMaxCand][kMetaThreads];
+  __shared__ int64_t red_sh[kMetaThreads / 64];
+  __shared__ int ok_sh[kMetaMaxCand];
+  __shared__ int last_part_sh;
+  const int t = threadIdx.x;
+  if (forced > 0) {
+    for (int i = t; i < batch; i += kMetaThreads) pg_sh[i] = seqlens[i];
+    __syncthreads();
+    if (t == 0) schedule_forced(pg_sh, batch, forced, sched, splits);
+    return;
+  }
+  int64_t part_total = 0;
+  for (int i = t; i < batch; i += kMetaThreads) {
+    const int n = pages_of(seqlens[i]);
+    pg_sh[i] = n;
+    part_total += n + f;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) part_total += __shfl_xor(part_total, off);
+  if ((t & 63) == 0) red_sh[t >> 6] = part_total;
   __syncthreads();
-  if (threadIdx.x != 0) return;
-  if (forced > 0)
-    schedule_forced(len_sh, batch, forced, sched, splits);
-  else
-    schedule_balanced(len_sh, batch, num_parts, fixed_overhead, sched, splits);
+  int64_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kMetaThreads / 64; ++w) total += red_sh[w];
+  int64_t lo, hi;
+  payload_bounds(total, num_parts, f, &lo, &hi);
+  const int ncand = min_payload ? (int)(hi - lo) + 1 : 1;  // <= kMetaMaxCand (host-checked)
+  const int chunk = (batch + kMetaThreads - 1) / kMetaThreads;
+  if (t < ncand) {
+    const int64_t T = min_payload ? lo + t : hi;
+    PackState st{T, 0, 0};
+    bool ok = true;
+    for (int c = 0; c < kMetaThreads; ++c) {
+      st_sh[t][c] = st;
+      const int e = min(batch, (c + 1) * chunk);
+      for (int b = c * chunk; ok && b < e; ++b)
+        ok = pack_sequence(b, pg_sh[b], T, f, st, NoEmit{}) && st.part < num_parts;
+    }
+    ok_sh[t] = ok ? 1 : 0;
+  }
+  __syncthreads();
+  int best = ncand - 1;  // the largest candidate (hi) always fits
+  for (int i = ncand - 1; i >= 0; --i)
+    if (ok_sh[i]) best = i;
+  const int64_t T = min_payload ? lo + best : hi;
+  PackState st = st_sh[best][t];
+  if (t == 0) {  // part 0 begins at the first page; its end is written by whoever closes it
+    sched[0] = 0;
+    sched[1] = 0;
+    sched[4] = 0;
+    splits[0] = 0;
+  }
+  const auto emit = [&](int p, int b, int page, int split) {
+    if (p < num_parts) {
+      int32_t* rec = sched + p * kSchedWords;
+      rec[0] = b;
+      rec[1] = page;
+      rec[4] = split;
+    }
+    if (p - 1 < num_parts) {
+      sched[(p - 1) * kSchedWords + 2] = b;
+      sched[(p - 1) * kSchedWords + 3] = page;
+    }
+  };
+  const int e = min(batch, (t + 1) * chunk);
+  for (int b = t * chunk; b < e; ++b) {
+    pack_sequence(b, pg_sh[b], T, f, st, emit);
+    splits[b + 1] = st.cum;
+  }
+  if (t == kMetaThreads - 1) last_part_sh = st.part;  // the last chunk ends at the final state
+  __syncthreads();
+  const int last = last_part_sh;
+  for (int p = t; p < num_parts; p += kMetaThreads) {
+    int32_t* rec = sched + p * kSchedWords;
+    if (p > last) {
+      sched_write(rec, batch, 0, batch, 0, 0);
+    } else {
+      if (p == last) {
+        rec[2] = batch;
+        rec[3] = 0;
+      }
+      rec[5] = 0;
+      rec[6] = 0;
+      rec[7] = 0;
+    }
+  }
 }
 
 }  // namespace mla
@@ -949,7 +1078,7 @@ mla::KParams make_params(const mla_decode_args* a) {
   const int64_t rows = (int64_t)a->s_q * a->heads_q;
   const int64_t slots = (int64_t)a->batch + a->num_parts;
   k.ws_lse = (float*)a->workspace;
-  k.ws_o = (float*)((char*)a->workspace + ws_lse_bytes(slots, rows));
+  k.ws_o = (uint16_t*)((char*)a->workspace + ws_lse_bytes(slots, rows));
   k.batch = a->batch;
   k.s_q = a->s_q;
   k.heads = a->heads_q;
@@ -960,14 +1089,17 @@ mla::KParams make_params(const mla_decode_args* a) {
   return k;
 }
 
-int launch_combine(const mla::KParams& k, int dtype, int copy_single, hipStream_t st) {
+// Partials are the 16-bit workspace rows of the decode path (PT = uint16_t) or the caller's
+// fp32 rows of mla_merge_partials (PT = float).
+template <typename PT>
+int launch_combine(const mla::KParams& k, const PT* part_o, int dtype, int copy_single, hipStream_t st) {
   dim3 grid(k.batch, (k.rows + 3) / 4);
   if (dtype == MLA_DTYPE_BF16)
-    hipLaunchKernelGGL(mla::mla_combine_kernel<MLA_DTYPE_BF16>, grid, dim3(256), 0, st, k.ws_o,
+    hipLaunchKernelGGL((mla::mla_combine_kernel<MLA_DTYPE_BF16, PT>), grid, dim3(256), 0, st, part_o,
                        k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
                        k.lse, copy_single);
   else
-    hipLaunchKernelGGL(mla::mla_combine_kernel<MLA_DTYPE_F16>, grid, dim3(256), 0, st, k.ws_o,
+    hipLaunchKernelGGL((mla::mla_combine_kernel<MLA_DTYPE_F16, PT>), grid, dim3(256), 0, st, part_o,
                        k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
                        k.lse, copy_single);
   const hipError_t e = hipGetLastError();
@@ -1020,9 +1152,10 @@ int mla_get_metadata_host(const int32_t* cache_seqlens, int32_t batch, int32_t n
     mla::schedule_forced(cache_seqlens, batch, forced_splits, tile_sched, num_splits);
   } else {
     if (num_parts < 1) return fail(MLA_ERR_INVALID, "num_parts must be >= 1");
-    mla::schedule_balanced(cache_seqlens, batch, num_parts,
-                           fixed_overhead < 0 ? mla::kDefaultFixedOverhead : fixed_overhead,
-                           tile_sched, num_splits);
+    std::vector<int32_t> pages(batch);
+    mla::schedule_packed(cache_seqlens, batch, num_parts,
+                         fixed_overhead < 0 ? mla::kDefaultSplitOverhead : fixed_overhead,
+                         fixed_overhead < 0, pages.data(), tile_sched, num_splits);
   }
   return MLA_OK;
 }
@@ -1038,10 +1171,11 @@ int mla_get_metadata(const int32_t* cache_seqlens, int32_t batch, int32_t num_pa
   } else if (num_parts < 1) {
     return fail(MLA_ERR_INVALID, "num_parts must be >= 1");
   }
-  hipLaunchKernelGGL(mla::mla_metadata_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream,
-                     cache_seqlens, batch, num_parts,
-                     fixed_overhead < 0 ? mla::kDefaultFixedOverhead : fixed_overhead,
-                     forced_splits, tile_sched, num_splits);
+  // min-payload candidates: kDefaultSplitOverhead + 1 <= kMetaMaxCand (static_assert)
+  hipLaunchKernelGGL(mla::mla_metadata_kernel, dim3(1), dim3(mla::kMetaThreads), 0,
+                     (hipStream_t)stream, cache_seqlens, batch, num_parts,
+                     fixed_overhead < 0 ? mla::kDefaultSplitOverhead : fixed_overhead,
+                     fixed_overhead < 0 ? 1 : 0, forced_splits, tile_sched, num_splits);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("metadata launch failed: ") + hipGetErrorString(e));
   return MLA_OK;
@@ -1051,13 +1185,14 @@ int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t
   if (batch < 1 || s_q < 1 || heads_q < 1 || num_parts < 1) return 0;
   const int64_t rows = (int64_t)s_q * heads_q;
   const int64_t slots = (int64_t)batch + num_parts;
-  return ws_lse_bytes(slots, rows) + slots * rows * mla::kDV * 4;
+  return ws_lse_bytes(slots, rows) + slots * rows * mla::kDV * 2;
 }
 
 int mla_decode_fwd(const mla_decode_args* args, void* stream) {
   const int rc = mla_splitkv_fwd(args, stream);
   if (rc != MLA_OK) return rc;
-  return launch_combine(make_params(args), args->dtype, 0, (hipStream_t)stream);
+  const mla::KParams kp = make_params(args);
+  return launch_combine(kp, (const uint16_t*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
 }
 
 int mla_splitkv_fwd(const mla_decode_args* args, void* stream) {
@@ -1079,7 +1214,8 @@ int mla_combine_fwd(const mla_decode_args* args, void* stream) {
   int64_t need = 0;
   const int rc = validate(args, &need);
   if (rc != MLA_OK) return rc;
-  return launch_combine(make_params(args), args->dtype, 0, (hipStream_t)stream);
+  const mla::KParams kp = make_params(args);
+  return launch_combine(kp, (const uint16_t*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
 }
 
 int mla_merge_partials(const float* part_o, const float* part_lse, const int32_t* num_splits,
@@ -1090,7 +1226,6 @@ int mla_merge_partials(const float* part_o, const float* part_lse, const int32_t
   if (dtype != MLA_DTYPE_BF16 && dtype != MLA_DTYPE_F16) return fail(MLA_ERR_INVALID, "bad dtype");
   if (!aligned(part_o, 16) || !aligned(out, 16)) return fail(MLA_ERR_INVALID, "part_o and out must be 16-byte aligned");
   mla::KParams k{};
-  k.ws_o = (float*)part_o;
   k.ws_lse = (float*)part_lse;
   k.splits = num_splits;
   k.batch = batch;
@@ -1102,7 +1237,7 @@ int mla_merge_partials(const float* part_o, const float* part_lse, const int32_t
   k.o_ss = 0;
   k.o_sh = mla::kDV;
   k.lse = lse_out;
-  return launch_combine(k, dtype, 1, (hipStream_t)stream);
+  return launch_combine(k, part_o, dtype, 1, (hipStream_t)stream);
 }
 
 int mla_split_plan(int32_t seqlen_kv, int32_t num_split, int32_t block_n, int32_t spread,

@@ -4,12 +4,16 @@
 // device (mla_get_metadata's single-workgroup kernel), so the schedule the GPU uses is
 // the schedule the CPU tests check.
 //
-// The balanced mode follows the algorithm described in the reference's
-// docs/num_split_design.md:49-104 (FlashMLA's get_mla_metadata): every part receives
-// about total/num_parts 64-token pages plus a fixed per-split overhead, filled greedily
-// in (sequence, page) order, cutting a sequence only when the rest of it does not fit.
-// The forced mode reproduces the reference's per-sequence split rule (_split_plan,
-// spread family, mla_decode.py:9-30) at page granularity.
+// Packing follows the algorithm described in the reference's docs/num_split_design.md:49-104
+// (FlashMLA's get_mla_metadata): parts are filled greedily in (sequence, page) order up to a
+// payload, a split costing its pages plus a fixed per-split overhead f, and a sequence is cut
+// only when the rest of it does not fit.  Two payloads:
+//   balanced     payload = ceil(total / num_parts) + f, the reference's rule;
+//   min-payload  the smallest payload in [ceil(total / num_parts), that value] whose packing
+//                fits in num_parts parts, i.e. the shortest critical part the greedy rule
+//                allows (the library default).
+// total = sum over sequences of (pages + f).  The forced mode reproduces the reference's
+// per-sequence split rule (_split_plan, spread family, mla_decode.py:9-30) at page granularity.
 //
 // Part record (MLA_SCHED_WORDS int32 words):
 //   [0] begin_b   [1] begin_page   [2] end_b   [3] end_page   [4] split index of the
@@ -22,6 +26,8 @@
 #pragma once
 #include <stdint.h>
 
+#include "mla_decode_amd.h"
+
 #if defined(__HIPCC__)
 #define MLA_HD __host__ __device__
 #else
@@ -32,9 +38,10 @@ namespace mla {
 
 constexpr int kPageTokens = 64;
 constexpr int kSchedWords = 8;
-// Per-split overhead in pages used when the caller passes a negative value: a split
-// re-reads the query tile, writes one fp32 partial row block and adds one combine input.
-constexpr int kDefaultFixedOverhead = 5;
+// Per-split overhead f in pages for the default (min-payload) schedule: a split re-reads the
+// query tile, writes one partial row block and adds one combine input.
+constexpr int kDefaultSplitOverhead = MLA_DEFAULT_SPLIT_OVERHEAD;
+static_assert(kDefaultSplitOverhead >= 0 && kDefaultSplitOverhead < 8, "candidate payload count");
 
 MLA_HD inline int pages_of(int32_t seqlen) {
   return seqlen > 0 ? (seqlen + kPageTokens - 1) / kPageTokens : 0;
@@ -51,39 +58,108 @@ MLA_HD inline void sched_write(int32_t* rec, int bb, int bp, int eb, int ep, int
   rec[7] = 0;
 }
 
-// Balanced greedy packing over num_parts parts.  Returns the number of workspace slots.
-MLA_HD inline int schedule_balanced(const int32_t* seqlens, int batch, int num_parts,
-                                    int fixed_overhead, int32_t* sched, int32_t* num_splits) {
-  int64_t total = 0;
-  for (int b = 0; b < batch; ++b) total += pages_of(seqlens[b]) + fixed_overhead;
-  const int64_t payload = (total + num_parts - 1) / num_parts + fixed_overhead;
-  int now_b = 0, now_page = 0, now_split = 0, cum = 0;
+// Greedy packing state between sequences: the part being filled, its unused payload and the
+// number of splits (workspace slots) so far.
+struct PackState {
+  int64_t remain;
+  int32_t part;
+  int32_t cum;
+};
+
+// One sequence b of n pages through the greedy packing with payload T and per-split overhead
+// f: the inner loop of docs/num_split_design.md:49-104 in closed form (the parts after a cut
+// each take T - f pages until the rest fits).  emit(part, b, first_page, split) is called for
+// every part that begins inside the sequence, in order.  Returns false if the packing cannot
+// place the sequence (T - f < 1 and it does not fit a fresh part).
+struct NoEmit {
+  MLA_HD void operator()(int, int, int, int) const {}
+};
+template <class Emit>
+MLA_HD inline bool pack_sequence(int b, int n, int64_t T, int f, PackState& st, const Emit& emit) {
+  if (st.remain >= (int64_t)n + f) {  // the whole sequence fits the current part
+    st.remain -= (int64_t)n + f;
+    st.cum += 1;
+    return true;
+  }
+  const int64_t take0 = st.remain - f;  // < n here
+  int64_t page = take0 > 0 ? take0 : 0;
+  int64_t split = take0 > 0 ? 1 : 0;
+  st.part += 1;
+  emit(st.part, b, (int)page, (int)split);
+  int64_t left = n - page;
+  if (T < left + f) {
+    const int64_t c = T - f;
+    if (c < 1) return false;
+    const int64_t k = (left + c - 1) / c - 1;  // >= 1 continuation parts of c pages
+    for (int64_t j = 1; j <= k; ++j) emit(st.part + (int)j, b, (int)(page + j * c), (int)(split + j));
+    st.part += (int)k;
+    page += k * c;
+    split += k;
+    left -= k * c;
+  }
+  st.remain = T - left - f;
+  st.cum += (int)split + 1;
+  return true;
+}
+
+// Sum over sequences of pages + f, and the payload bounds [lo, hi]: no packing fits num_parts
+// parts below lo, and the greedy packing always fits at hi (every closed part consumes at
+// least hi - f of the total).
+MLA_HD inline void payload_bounds(int64_t total, int num_parts, int f, int64_t* lo, int64_t* hi) {
+  *lo = (total + num_parts - 1) / num_parts;
+  *hi = *lo + f;
+}
+
+// Does the greedy packing with payload T fit in num_parts parts?
+MLA_HD inline bool packing_fits(const int32_t* pages, int batch, int num_parts, int64_t T, int f) {
+  PackState st{T, 0, 0};
+  for (int b = 0; b < batch; ++b)
+    if (!pack_sequence(b, pages[b], T, f, st, NoEmit{}) || st.part >= num_parts) return false;
+  return true;
+}
+
+// Writes the records and num_splits of the greedy packing with payload T (which must fit).
+// Parts after the last used one are empty records at (batch, 0).  Returns the slot count.
+MLA_HD inline int write_packing(const int32_t* pages, int batch, int num_parts, int64_t T, int f,
+                                int32_t* sched, int32_t* num_splits) {
+  sched_write(sched, 0, 0, batch, 0, 0);
+  const auto emit = [&](int p, int b, int page, int split) {
+    if (p < num_parts) sched_write(sched + p * kSchedWords, b, page, batch, 0, split);
+    if (p - 1 < num_parts) {
+      sched[(p - 1) * kSchedWords + 2] = b;
+      sched[(p - 1) * kSchedWords + 3] = page;
+    }
+  };
+  PackState st{T, 0, 0};
   num_splits[0] = 0;
-  for (int p = 0; p < num_parts; ++p) {
-    const int begin_b = now_b, begin_page = now_page, first_split = now_split;
-    // The last part takes whatever is left, so every page is always covered.
-    int64_t remain = (p == num_parts - 1) ? (int64_t)1 << 60 : payload;
-    while (now_b < batch) {
-      const int left = pages_of(seqlens[now_b]) - now_page;
-      if (remain >= (int64_t)left + fixed_overhead) {
-        cum += now_split + 1;
-        num_splits[now_b + 1] = cum;
-        remain -= (int64_t)left + fixed_overhead;
-        ++now_b;
-        now_page = 0;
-        now_split = 0;
-      } else {
-        const int64_t take = remain - fixed_overhead;
-        if (take > 0) {
-          now_page += (int)take;
-          ++now_split;
-        }
+  for (int b = 0; b < batch; ++b) {
+    pack_sequence(b, pages[b], T, f, st, emit);
+    num_splits[b + 1] = st.cum;
+  }
+  for (int p = st.part + 1; p < num_parts; ++p) sched_write(sched + p * kSchedWords, batch, 0, batch, 0, 0);
+  return st.cum;
+}
+
+// Host driver of both payload rules (pages computed into a scratch array of batch entries).
+// min_payload = false: the reference's payload; true: the smallest payload that fits.
+inline int schedule_packed(const int32_t* seqlens, int batch, int num_parts, int f,
+                           bool min_payload, int32_t* pages, int32_t* sched,
+                           int32_t* num_splits) {
+  int64_t total = 0;
+  for (int b = 0; b < batch; ++b) {
+    pages[b] = pages_of(seqlens[b]);
+    total += pages[b] + f;
+  }
+  int64_t lo, hi;
+  payload_bounds(total, num_parts, f, &lo, &hi);
+  int64_t T = hi;
+  if (min_payload)
+    for (int64_t c = lo; c < hi; ++c)
+      if (packing_fits(pages, batch, num_parts, c, f)) {
+        T = c;
         break;
       }
-    }
-    sched_write(sched + p * kSchedWords, begin_b, begin_page, now_b, now_page, first_split);
-  }
-  return cum;
+  return write_packing(pages, batch, num_parts, T, f, sched, num_splits);
 }
 
 // Every sequence cut into min(forced, pages) near-equal contiguous page ranges; the first

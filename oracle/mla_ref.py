@@ -13,6 +13,9 @@ Functions and the reference code they follow:
   * ``split_plan``         -- mla_decode.py:9-30.
   * ``schedule_balanced`` / ``schedule_forced`` -- the tile schedule: the greedy packing
     described in docs/num_split_design.md:49-104 and the spread rule of mla_decode.py:9-30.
+  * ``pack_greedy`` / ``schedule_min_payload`` -- the same greedy loop at an explicit payload
+    (no catch-all last part), and the smallest payload in [ceil(total/parts),
+    ceil(total/parts) + f] whose packing fits (the library's default schedule).
 
 Pinning (tests/test_oracle.py): ``decode_paged`` against torch's
 ``scaled_dot_product_attention`` in float64 (a library routine), closed forms (L = 1,
@@ -136,6 +139,48 @@ def schedule_balanced(seqlens: List[int], num_parts: int, fixed_overhead: int):
                 break
         recs.append((begin[0], begin[1], now_b, now_p, begin[2]))
     return recs, prefix
+
+
+def pack_greedy(seqlens: List[int], num_parts: int, payload: int, fixed_overhead: int):
+    """The loop of ``schedule_balanced`` with every part, the last included, limited to
+    ``payload``.  Returns (records, prefix), or None if the pages do not fit in num_parts
+    parts (or the loop stops making progress)."""
+    B = len(seqlens)
+    f = fixed_overhead
+    now_b = now_p = now_split = cum = 0
+    prefix = [0] * (B + 1)
+    recs = []
+    for p in range(num_parts):
+        begin = (now_b, now_p, now_split)
+        remain = payload
+        while now_b < B:
+            left = pages_of(seqlens[now_b]) - now_p
+            if remain >= left + f:
+                cum += now_split + 1
+                prefix[now_b + 1] = cum
+                remain -= left + f
+                now_b, now_p, now_split = now_b + 1, 0, 0
+            else:
+                take = remain - f
+                if take > 0:
+                    now_p += take
+                    now_split += 1
+                break
+        recs.append((begin[0], begin[1], now_b, now_p, begin[2]))
+    if now_b < B:
+        return None
+    return recs, prefix
+
+
+def schedule_min_payload(seqlens: List[int], num_parts: int, fixed_overhead: int):
+    """First payload in [lo, lo + f] (lo = ceil(total / parts)) whose greedy packing fits."""
+    total = sum(pages_of(L) + fixed_overhead for L in seqlens)
+    lo = -(-total // num_parts)
+    for payload in range(lo, lo + fixed_overhead + 1):
+        got = pack_greedy(seqlens, num_parts, payload, fixed_overhead)
+        if got is not None:
+            return got[0], got[1], payload
+    raise AssertionError("the reference payload always fits")
 
 
 def schedule_forced(seqlens: List[int], forced: int):

@@ -69,6 +69,12 @@ def test_host_schedule_matches_oracle(seed):
             assert sched[:, :5].tolist() == [list(r) for r in recs]
             assert torch.all(sched[:, 5:] == 0)
             assert splits.tolist() == prefix
+        # the default (fixed_overhead < 0): min-payload packing at the default overhead
+        sched, splits = get_mla_metadata_host(lengths, parts, -1)
+        recs, prefix, _ = R.schedule_min_payload(lengths, parts, _lib.MLA_DEFAULT_SPLIT_OVERHEAD)
+        assert sched[:, :5].tolist() == [list(r) for r in recs]
+        assert torch.all(sched[:, 5:] == 0)
+        assert splits.tolist() == prefix
     for forced in (1, 3, 8):
         sched, splits = get_mla_metadata_host(lengths, 0, forced_splits=forced)
         recs, prefix = R.schedule_forced(lengths, forced)
@@ -79,7 +85,8 @@ def test_host_schedule_matches_oracle(seed):
 def test_workspace_bytes(lib):
     n = lib.mla_workspace_bytes(64, 1, 128, 128)
     slots, rows = 64 + 128, 128
-    assert n == -(-slots * rows * 4 // 256) * 256 + slots * rows * 512 * 4
+    # fp32 lse per (slot, row) padded to 256 bytes, then 16-bit partial rows of 512
+    assert n == -(-slots * rows * 4 // 256) * 256 + slots * rows * 512 * 2
     assert lib.mla_workspace_bytes(0, 1, 16, 4) == 0
 
 

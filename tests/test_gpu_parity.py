@@ -6,6 +6,7 @@ Full-size benchmark configs are checked on a sample of their sequences (oracle c
 whole-output properties.
 """
 import math
+import random
 import sys
 
 import pytest
@@ -172,15 +173,23 @@ def test_golden_fixtures_on_gpu(gpu):
 
 
 def test_schedule_device_matches_host(gpu):
-    lengths = [0, 1, 4096, 65, 16384, 128, 7000]
-    seq = torch.tensor(lengths, dtype=torch.int32, device=gpu)
-    for parts, fo, forced in ((256, -1, 0), (7, 0, 0), (0, -1, 3)):
-        say(f"schedule parts={parts} fo={fo} forced={forced}")
-        s_d, n_d = get_mla_metadata(seq, 16, 1, num_parts=parts or None, fixed_overhead=fo,
-                                    forced_splits=forced)
-        s_h, n_h = get_mla_metadata_host(lengths, parts, fo, forced)
-        torch.cuda.synchronize()
-        assert torch.equal(s_d.cpu(), s_h) and torch.equal(n_d.cpu(), n_h)
+    rng = random.Random(5)
+    cases = [
+        [0, 1, 4096, 65, 16384, 128, 7000],
+        [4096] * 64,
+        # more sequences than the metadata kernel's threads: several per replay chunk
+        [rng.choice([0, 1, 64, rng.randint(1, 9000)]) for _ in range(700)],
+    ]
+    for lengths in cases:
+        seq = torch.tensor(lengths, dtype=torch.int32, device=gpu)
+        for parts, fo, forced in ((256, -1, 0), (1024, -1, 0), (1, -1, 0), (7, 0, 0), (256, 5, 0),
+                                  (0, -1, 3)):
+            say(f"schedule B={len(lengths)} parts={parts} fo={fo} forced={forced}")
+            s_d, n_d = get_mla_metadata(seq, 16, 1, num_parts=parts or None, fixed_overhead=fo,
+                                        forced_splits=forced)
+            s_h, n_h = get_mla_metadata_host(lengths, parts, fo, forced)
+            torch.cuda.synchronize()
+            assert torch.equal(s_d.cpu(), s_h) and torch.equal(n_d.cpu(), n_h)
 
 
 def test_flash_mla_call_shape(gpu):

@@ -201,6 +201,46 @@ def test_balanced_schedule_bruteforce(seed):
                     assert pe - pb <= payload
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_min_payload_schedule_bruteforce(seed):
+    """The default schedule: a valid cover, every part within the chosen payload, and no
+    smaller payload fits; the explicit-payload loop agrees with the reference loop where
+    both apply."""
+    rng = random.Random(50 + seed)
+    B = rng.choice([1, 3, 17, 64, 132])
+    lengths = [rng.choice([0, 1, 63, 64, 65, rng.randint(1, 20000)]) for _ in range(B)]
+    for parts in (1, 7, 64, 256, 1024):
+        for fo in (0, 1, 2, 5):
+            recs, prefix, payload = R.schedule_min_payload(lengths, parts, fo)
+            assert len(recs) == parts
+            _check_schedule(lengths, recs, prefix, parts)
+            total = sum(R.pages_of(L) + fo for L in lengths)
+            lo = -(-total // parts)
+            assert lo <= payload <= lo + fo
+            if payload > lo:
+                assert R.pack_greedy(lengths, parts, payload - 1, fo) is None
+            cost = [0] * parts
+            for p, b, pb, pe, sp in R.segments(recs, lengths):
+                cost[p] += pe - pb + fo
+            assert max(cost) <= payload
+            # at the reference payload the explicit loop is the reference loop
+            bal = R.schedule_balanced(lengths, parts, fo)
+            assert R.pack_greedy(lengths, parts, lo + fo, fo) == bal
+
+
+def test_min_payload_uniform_closed_form():
+    """Uniform lengths with parts = k * batch: every part is exactly pages / k pages of one
+    sequence (the shape of the B=64, L=4096 decode on 256 parts)."""
+    for B, L, k, fo in ((64, 4096, 4, 2), (64, 4096, 4, 5), (32, 16384, 4, 2), (8, 1024, 2, 0)):
+        recs, prefix, payload = R.schedule_min_payload([L] * B, B * k, fo)
+        per = R.pages_of(L) // k
+        assert payload == per + fo
+        assert prefix == [k * b for b in range(B + 1)]
+        assert recs == [(i // k, (i % k) * per, i // k, (i % k + 1) * per, i % k)
+                        if (i % k) < k - 1 else (i // k, (i % k) * per, i // k + 1, 0, i % k)
+                        for i in range(B * k)]
+
+
 def test_forced_schedule_bruteforce():
     lengths = [0, 1, 64, 65, 1000, 4096]
     for forced in (1, 2, 3, 8):
