@@ -53,7 +53,7 @@ extern "C" {
 /* Each part of the tile schedule is described by this many int32 words. */
 #define MLA_SCHED_WORDS 8
 /* Per-split overhead, in pages, of the default (min-payload) tile schedule. */
-#define MLA_DEFAULT_SPLIT_OVERHEAD 2
+#define MLA_DEFAULT_SPLIT_OVERHEAD 3
 
 /*
  * Decode arguments.  Strides are in elements.  The latent ("nope", dims

@@ -15,7 +15,7 @@ from .build import LIB_PATH
 MLA_DTYPE_BF16 = 0
 MLA_DTYPE_F16 = 1
 MLA_SCHED_WORDS = 8
-MLA_DEFAULT_SPLIT_OVERHEAD = 2  # pages; the default schedule's per-split overhead
+MLA_DEFAULT_SPLIT_OVERHEAD = 3  # pages; the default schedule's per-split overhead
 MLA_DIM_QK = 576
 MLA_DIM_V = 512
 MLA_PAGE_TOKENS = 64

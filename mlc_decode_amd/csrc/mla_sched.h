@@ -90,7 +90,11 @@ MLA_HD inline bool pack_sequence(int b, int n, int64_t T, int f, PackState& st, 
   if (T < left + f) {
     const int64_t c = T - f;
     if (c < 1) return false;
-    const int64_t k = (left + c - 1) / c - 1;  // >= 1 continuation parts of c pages
+    // >= 1 continuation parts of c pages (32-bit division whenever the operands fit, which
+    // they do for any real cache: a 64-bit division is a long software sequence on the GPU)
+    const int64_t k = (left < (1ll << 31) && c < (1ll << 31))
+                          ? (int64_t)(((uint32_t)left + (uint32_t)c - 1u) / (uint32_t)c) - 1
+                          : (left + c - 1) / c - 1;
     for (int64_t j = 1; j <= k; ++j) emit(st.part + (int)j, b, (int)(page + j * c), (int)(split + j));
     st.part += (int)k;
     page += k * c;
