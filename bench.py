@@ -36,6 +36,9 @@ def parse():
     ap.add_argument("--record", default="", metavar="PATH",
                     help="with --all-configs: write the per-config record (tile, splits, timings, "
                          "roofline) as JSON, the MI355X counterpart of mla_best_configs.json")
+    ap.add_argument("--append", action="store_true",
+                    help="measure the paged KV-cache append (mla_kv_append) at every config's "
+                         "batch and s_q instead of the decode; one JSON line per config")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain MIB-MiB device copy 3x (scale for FETCH/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -155,6 +158,46 @@ def cpu_baseline(m, budget_s):
                       f"scaled by token count; fp32 torch on {cpu_model()}"}
 
 
+def measure_append(cfg_name, steps):
+    """mla_kv_append of s_q new tokens per sequence into the config's paged cache (two spare
+    pages per sequence, so `steps` successive appends stay inside the table)."""
+    import torch
+    from mlc_decode_amd.api import kv_append
+    from mlc_decode_amd.inputs import CONFIGS, make_inputs
+    cfg = CONFIGS[cfg_name]
+    inp = make_inputs(cfg, seed=0)
+    B, n_new = cfg.batch, cfg.s_q
+    nb = inp.kv_cache.shape[0]
+    spare = torch.arange(nb, nb + 2 * B, dtype=torch.int32).view(B, 2)
+    lens = inp.cache_seqlens.clone()
+    P = int(((lens + 63) // 64).max()) + 2
+    bt = torch.zeros(B, P, dtype=torch.int32)
+    for b in range(B):
+        n = (int(lens[b]) + 63) // 64
+        bt[b, :n] = inp.block_table[b, :n]
+        bt[b, n:n + 2] = spare[b]
+    cache = torch.zeros(nb + 2 * B, 64, 1, 576, dtype=cfg.dtype, device="cuda:0")
+    cache[:nb] = inp.kv_cache.to("cuda:0")
+    new = torch.randn(B, n_new, 576).to(cfg.dtype).to("cuda:0")
+    btg, lg = bt.to("cuda:0"), lens.to("cuda:0")
+    steps = min(steps, 64 // n_new)
+    stream = torch.cuda.current_stream()
+    import ctypes
+    from mlc_decode_amd import _lib
+    args = kv_append(new, cache, btg, lg)
+    torch.cuda.synchronize()
+    steps = (steps - 1) // 2
+    ms = time_gpu(lambda: kv_append(new, cache, btg, lg), steps, 0, stream)
+    lib, ap, sp = _lib.load(), ctypes.byref(args), stream.cuda_stream
+    ms_c = time_gpu(lambda: _lib.check("mla_kv_append", lib.mla_kv_append(ap, sp)), steps, 0, stream)
+    nbytes = B * n_new * 576 * 2 * 2 + B * 4 * 2  # rows read + written, lengths read + written
+    return {"op": "kv_append", "config": cfg_name, "batch": B, "n_new": n_new,
+            "us_call": round(ms * 1e3, 3), "us_c_abi": round(ms_c * 1e3, 3), "bytes": nbytes,
+            "gbs": round(nbytes / (ms_c * 1e-3) / 1e9, 2),
+            "note": "launch-bound: a few hundred KB per call; us_call is the Python API, us_c_abi "
+                    "the C entry point with its arguments prepared once"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -164,6 +207,10 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if args.append:
+        for name in ("C1", "C2", "C3", "C4", "C5"):
+            print(json.dumps(measure_append(name, args.steps)), flush=True)
+        return
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20)
         src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)

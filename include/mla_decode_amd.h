@@ -221,6 +221,40 @@ int mla_launch(const void* q, const void* q_pe, const void* kv, const void* k_pe
                const int32_t* num_splits, void* workspace, int64_t workspace_bytes,
                void* stream);
 
+/*
+ * Paged KV-cache append: the step before decode that writes the new tokens' latent + rope rows
+ * into the paged cache and advances cache_seqlens.  The reference decodes a pre-filled cache
+ * and has no append; this is the next row of its path (the cache layout it consumes).  For
+ * every sequence b and new token t < n_new:
+ *   pos = cache_seqlens[b] + t,  page = block_table[b * block_table_stride + pos / 64],
+ *   cache row (page, pos % 64) <- kv_new[b, t, 0..575]   (dims 0..511 latent, 512..575 rope)
+ * then cache_seqlens[b] += n_new, in place on the device.  The pages must already be assigned
+ * in block_table: if any of a sequence's new positions has pos / 64 >= max_pages or a page id
+ * outside [0, num_blocks), none of its rows is written, its length is not advanced and
+ * *status (if non-NULL) is set to 1 (the caller clears it).  The cache halves are addressed
+ * as in mla_decode_args (one tensor or two views).  Returns 0, MLA_ERR_INVALID (bad shape,
+ * pointer, alignment or stride; nothing is launched) or MLA_ERR_HIP.
+ */
+typedef struct mla_kv_append_args {
+  int32_t batch;   /* B >= 1 */
+  int32_t n_new;   /* new tokens per sequence, 1 .. 64 */
+  int32_t dtype;   /* MLA_DTYPE_BF16 or MLA_DTYPE_F16 (kv_new and the cache) */
+  int32_t num_blocks;
+  const void* kv_new;  /* [B, n_new, 576], dims contiguous */
+  int64_t new_stride_b, new_stride_t;
+  void* kv_nope;       /* cache latent half: page / token strides as in mla_decode_args */
+  void* kv_rope;       /* cache rope half */
+  int64_t kv_stride_page, kv_stride_tok;
+  int64_t kv_rope_stride_page, kv_rope_stride_tok;
+  const int32_t* block_table; /* [B, max_pages] */
+  int32_t block_table_stride;
+  int32_t max_pages;
+  int32_t* cache_seqlens;     /* [B], advanced in place */
+  int32_t* status;            /* optional device word, set to 1 on a skipped sequence */
+} mla_kv_append_args;
+
+int mla_kv_append(const mla_kv_append_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,7 +3,7 @@
 The hot path is hand-written HIP (``csrc/mla_decode.hip``) reached through the C ABI of
 ``include/mla_decode_amd.h``; this package is the torch-side host code around it.
 """
-from .api import (flash_mla_with_kvcache, get_mla_metadata, get_mla_metadata_host,
+from .api import (flash_mla_with_kvcache, get_mla_metadata, get_mla_metadata_host, kv_append,
                   merge_partials, mla_decode_with_kvcache, num_parts_for)
 from .legacy import MlaKernel
 
@@ -11,6 +11,7 @@ __all__ = [
     "flash_mla_with_kvcache",
     "get_mla_metadata",
     "get_mla_metadata_host",
+    "kv_append",
     "merge_partials",
     "mla_decode_with_kvcache",
     "num_parts_for",

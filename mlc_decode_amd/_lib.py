@@ -35,6 +35,7 @@ EXPORTED = (
     "mla_merge_partials",
     "mla_split_plan",
     "mla_launch",
+    "mla_kv_append",
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -82,6 +83,31 @@ class MlaDecodeArgs(ctypes.Structure):
         ("lse", _vp),
         ("workspace", _vp),
         ("workspace_bytes", _i64),
+    ]
+
+
+class MlaKvAppendArgs(ctypes.Structure):
+    """Layout of ``mla_kv_append_args`` (include/mla_decode_amd.h)."""
+
+    _fields_ = [
+        ("batch", _i32),
+        ("n_new", _i32),
+        ("dtype", _i32),
+        ("num_blocks", _i32),
+        ("kv_new", _vp),
+        ("new_stride_b", _i64),
+        ("new_stride_t", _i64),
+        ("kv_nope", _vp),
+        ("kv_rope", _vp),
+        ("kv_stride_page", _i64),
+        ("kv_stride_tok", _i64),
+        ("kv_rope_stride_page", _i64),
+        ("kv_rope_stride_tok", _i64),
+        ("block_table", _vp),
+        ("block_table_stride", _i32),
+        ("max_pages", _i32),
+        ("cache_seqlens", _vp),
+        ("status", _vp),
     ]
 
 
@@ -140,6 +166,8 @@ def load() -> ctypes.CDLL:
         lib.mla_launch.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp,
                                    _i32, _vp, _vp, _i64, _vp]
         lib.mla_launch.restype = ctypes.c_int
+        lib.mla_kv_append.argtypes = [ctypes.POINTER(MlaKvAppendArgs), _vp]
+        lib.mla_kv_append.restype = ctypes.c_int
         _lib = lib
         return lib
 

@@ -26,7 +26,8 @@ from typing import Optional, Sequence, Tuple, Union
 import torch
 
 from . import _lib
-from ._lib import MLA_DIM_QK, MLA_DIM_V, MLA_DTYPE_BF16, MLA_DTYPE_F16, MlaDecodeArgs, check
+from ._lib import (MLA_DIM_QK, MLA_DIM_V, MLA_DTYPE_BF16, MLA_DTYPE_F16, MlaDecodeArgs,
+                   MlaKvAppendArgs, check)
 
 _DTYPES = {torch.bfloat16: MLA_DTYPE_BF16, torch.float16: MLA_DTYPE_F16}
 
@@ -280,6 +281,56 @@ def merge_partials(part_o: torch.Tensor, part_lse: torch.Tensor, num_splits: tor
         part_o.data_ptr(), part_lse.data_ptr(), num_splits.data_ptr(), batch, rows,
         _DTYPES[dtype], out.data_ptr(), lse.data_ptr(), _stream_ptr(part_o.device)))
     return out, lse
+
+
+def kv_append(kv_new: torch.Tensor, kv_cache, block_table: torch.Tensor,
+              cache_seqlens: torch.Tensor, status: Optional[torch.Tensor] = None) -> MlaKvAppendArgs:
+    """Append ``kv_new [B, n_new, 576]`` (or ``[B, n_new, 1, 576]``) to the paged cache in
+    place and advance ``cache_seqlens`` by ``n_new`` (``mla_kv_append``).
+
+    Token t of sequence b goes to row ``(L_b + t) % 64`` of page
+    ``block_table[b, (L_b + t) // 64]``, L_b the length before the call; the pages must already
+    be assigned.  A sequence whose new positions run past the table or hit a page id outside
+    the cache is left untouched and sets ``status[0] = 1`` when a status tensor (int32, on the
+    device) is given.  Nothing is synchronised: the call is queued on the current stream.
+    Returns the filled C argument struct (for re-launching through the C ABI directly).
+    """
+    _require_gpu(kv_new, "kv_new")
+    latent, rope = _split_kv(kv_cache)
+    if kv_new.dim() == 4:
+        if kv_new.shape[2] != 1:
+            raise ValueError("kv_new [B, n_new, 1, 576] must have one KV head")
+        kv_new = kv_new[:, :, 0]
+    if kv_new.dim() != 3 or kv_new.shape[-1] != MLA_DIM_QK:
+        raise ValueError("kv_new must be [B, n_new, 576]")
+    if kv_new.dtype not in _DTYPES or latent.dtype != kv_new.dtype or rope.dtype != kv_new.dtype:
+        raise ValueError("kv_new and the cache must share one 16-bit dtype (bf16 or fp16)")
+    B, n_new = kv_new.shape[0], kv_new.shape[1]
+    if latent.dim() != 4 or latent.shape[1] != _lib.MLA_PAGE_TOKENS or latent.shape[2] != 1:
+        raise ValueError("kv_cache must be [num_blocks, 64, 1, 576] (or a latent / rope pair)")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B:
+        raise ValueError("block_table must be [B, max_pages] int32")
+    if cache_seqlens.dtype != torch.int32 or cache_seqlens.shape != (B,) or not cache_seqlens.is_contiguous():
+        raise ValueError("cache_seqlens must be a contiguous [B] int32 tensor")
+    if kv_new.stride(-1) != 1 or latent.stride(-1) != 1 or rope.stride(-1) != 1:
+        raise ValueError("the dims of kv_new and of the cache must be contiguous")
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 1):
+        raise ValueError("status must be an int32 tensor of at least one element")
+    for t, name in ((latent, "kv_cache"), (block_table, "block_table"), (cache_seqlens, "cache_seqlens")):
+        _require_gpu(t, name)
+    a = MlaKvAppendArgs()
+    a.batch, a.n_new, a.dtype, a.num_blocks = B, n_new, _DTYPES[kv_new.dtype], latent.shape[0]
+    a.kv_new = kv_new.data_ptr()
+    a.new_stride_b, a.new_stride_t = kv_new.stride(0), kv_new.stride(1)
+    a.kv_nope, a.kv_rope = latent.data_ptr(), rope.data_ptr()
+    a.kv_stride_page, a.kv_stride_tok = latent.stride(0), latent.stride(1)
+    a.kv_rope_stride_page, a.kv_rope_stride_tok = rope.stride(0), rope.stride(1)
+    a.block_table = block_table.data_ptr()
+    a.block_table_stride, a.max_pages = block_table.stride(0), block_table.shape[1]
+    a.cache_seqlens = cache_seqlens.data_ptr()
+    a.status = status.data_ptr() if status is not None else None
+    check("mla_kv_append", _lib.load().mla_kv_append(ctypes.byref(a), _stream_ptr(kv_new.device)))
+    return a
 
 
 def default_sm_scale() -> float:

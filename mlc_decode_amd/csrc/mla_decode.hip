@@ -726,6 +726,58 @@ void mla_splitkv_kernel(KParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// paged KV-cache append: one wave per sequence (its length is read once, before its rows are
+// written, and advanced after them); lanes 0..63 copy the 512 latent dims and lanes 0..7
+// the 64 rope dims of each new row, 16 bytes per lane
+// ---------------------------------------------------------------------------------------
+struct AppendParams {
+  const uint16_t* kv_new;
+  int64_t n_sb, n_st;
+  uint16_t* kv_nope;
+  uint16_t* kv_rope;
+  int64_t kv_sp, kv_st, kr_sp, kr_st;
+  const int32_t* block_table;
+  int32_t bt_stride, max_pages, num_blocks, batch, n_new;
+  int32_t* seqlens;
+  int32_t* status;
+};
+
+__global__ __launch_bounds__(256) void mla_kv_append_kernel(AppendParams a) {
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (b >= a.batch) return;  // whole waves only
+  const int L = a.seqlens[b];
+  bool ok = L >= 0;
+  for (int t = 0; t < a.n_new; ++t) {
+    const int pos = L + t;
+    const int pi = pos >> 6;
+    if (pi >= a.max_pages) {
+      ok = false;
+    } else {
+      const int pg = a.block_table[(int64_t)b * a.bt_stride + pi];
+      ok = ok && pg >= 0 && pg < a.num_blocks;
+    }
+  }
+  if (!ok) {
+    if (lane == 0 && a.status != nullptr) a.status[0] = 1;
+    return;
+  }
+  for (int t = 0; t < a.n_new; ++t) {
+    const int pos = L + t;
+    const int pg = a.block_table[(int64_t)b * a.bt_stride + (pos >> 6)];
+    const int row = pos & 63;
+    const uint16_t* src = a.kv_new + b * a.n_sb + t * a.n_st;
+    const i32x4 v = *(const i32x4*)(src + 8 * lane);
+    *(i32x4*)(a.kv_nope + (int64_t)pg * a.kv_sp + (int64_t)row * a.kv_st + 8 * lane) = v;
+    if (lane < 8) {
+      const i32x4 r = *(const i32x4*)(src + kRopeOff + 8 * lane);
+      *(i32x4*)(a.kv_rope + (int64_t)pg * a.kr_sp + (int64_t)row * a.kr_st + 8 * lane) = r;
+    }
+  }
+  if (lane == 0) a.seqlens[b] = L + a.n_new;
+}
+
+// ---------------------------------------------------------------------------------------
 // combine: LSE-weighted merge of the splits of each (sequence, row)
 // ---------------------------------------------------------------------------------------
 // Eight consecutive partial values of one row, widened to fp32: from the fp32 partials of
@@ -1305,6 +1357,40 @@ int mla_launch(const void* q, const void* q_pe, const void* kv, const void* k_pe
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
   return mla_decode_fwd(&a, stream);
+}
+
+int mla_kv_append(const mla_kv_append_args* a, void* stream) {
+  if (a == nullptr) return fail(MLA_ERR_INVALID, "args is NULL");
+  if (a->batch < 1 || a->n_new < 1 || a->n_new > mla::kPageTokens)
+    return fail(MLA_ERR_INVALID, "batch must be >= 1 and n_new in [1, 64]");
+  if (a->dtype != MLA_DTYPE_BF16 && a->dtype != MLA_DTYPE_F16)
+    return fail(MLA_ERR_INVALID, "dtype must be MLA_DTYPE_BF16 or MLA_DTYPE_F16");
+  if (!a->kv_new || !a->kv_nope || !a->kv_rope || !a->block_table || !a->cache_seqlens)
+    return fail(MLA_ERR_INVALID, "a required pointer is NULL");
+  if (!aligned(a->kv_new, 16) || !aligned(a->kv_nope, 16) || !aligned(a->kv_rope, 16))
+    return fail(MLA_ERR_INVALID, "kv_new / cache pointers must be 16-byte aligned");
+  const int64_t s8[] = {a->new_stride_b, a->new_stride_t, a->kv_stride_page, a->kv_stride_tok,
+                        a->kv_rope_stride_page, a->kv_rope_stride_tok};
+  for (int64_t v : s8)
+    if (v < 0 || v % 8) return fail(MLA_ERR_INVALID, "strides must be non-negative multiples of 8 elements");
+  if (a->block_table_stride < 1 || a->max_pages < 1 || a->num_blocks < 1)
+    return fail(MLA_ERR_INVALID, "block_table_stride, max_pages and num_blocks must be >= 1");
+  mla::AppendParams k{};
+  k.kv_new = (const uint16_t*)a->kv_new;
+  k.n_sb = a->new_stride_b; k.n_st = a->new_stride_t;
+  k.kv_nope = (uint16_t*)a->kv_nope; k.kv_rope = (uint16_t*)a->kv_rope;
+  k.kv_sp = a->kv_stride_page; k.kv_st = a->kv_stride_tok;
+  k.kr_sp = a->kv_rope_stride_page; k.kr_st = a->kv_rope_stride_tok;
+  k.block_table = a->block_table;
+  k.bt_stride = a->block_table_stride; k.max_pages = a->max_pages; k.num_blocks = a->num_blocks;
+  k.batch = a->batch; k.n_new = a->n_new;
+  k.seqlens = a->cache_seqlens;
+  k.status = a->status;
+  hipLaunchKernelGGL(mla::mla_kv_append_kernel, dim3((a->batch + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("kv append launch failed: ") + hipGetErrorString(e));
+  return MLA_OK;
 }
 
 }  // extern "C"

@@ -13,6 +13,9 @@ Functions and the reference code they follow:
   * ``split_plan``         -- mla_decode.py:9-30.
   * ``schedule_balanced`` / ``schedule_forced`` -- the tile schedule: the greedy packing
     described in docs/num_split_design.md:49-104 and the spread rule of mla_decode.py:9-30.
+  * ``append_paged``       -- the paged KV-cache append (no reference counterpart: the
+    reference decodes a pre-filled cache; the page/row mapping is the one ``gather``
+    reads, handmade/bench_metax_flashmla.py:53-61).
   * ``pack_greedy`` / ``schedule_min_payload`` -- the same greedy loop at an explicit payload
     (no catch-all last part), and the smallest payload in [ceil(total/parts),
     ceil(total/parts) + f] whose packing fits (the library's default schedule).
@@ -53,8 +56,32 @@ def decode_contiguous(q, q_pe, kv, k_pe, dtype=torch.float32):
 def gather(kv_cache: torch.Tensor, table_row: torch.Tensor, L: int) -> torch.Tensor:
     """The first L tokens of one sequence: [L, D] from pages table_row[0..ceil(L/64))."""
     n = (L + PAGE - 1) // PAGE
-    pages = kv_cache[table_row[:n].long()]          # [n, 64, 1, D]
-    return pages.reshape(n * PAGE, -1)[:L]
+    pages = kv_cache[table_row[:n].long()]          # [n, 64, D] (or [n, 64, 1, D])
+    return pages.reshape(n * PAGE, pages.shape[-1])[:L]
+
+
+def append_paged(kv_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
+                 kv_new: torch.Tensor):
+    """Write kv_new [B, n, 576] at positions L_b .. L_b+n-1 of each sequence and advance the
+    lengths.  A sequence with a position past the table or a page id outside the cache is left
+    untouched.  Returns (new cache, new lengths, list of skipped sequences); inputs unchanged."""
+    cache = kv_cache.clone()
+    lens = cache_seqlens.clone()
+    B, n = kv_new.shape[0], kv_new.shape[1]
+    P, N = block_table.shape[1], kv_cache.shape[0]
+    skipped = []
+    for b in range(B):
+        L = int(cache_seqlens[b])
+        slots = [(L + t) // PAGE for t in range(n)]
+        if L < 0 or any(pi >= P for pi in slots) or any(
+                not 0 <= int(block_table[b, pi]) < N for pi in slots):
+            skipped.append(b)
+            continue
+        for t in range(n):
+            pos = L + t
+            cache[int(block_table[b, pos // PAGE]), pos % PAGE, 0, :] = kv_new[b, t]
+        lens[b] = L + n
+    return cache, lens, skipped
 
 
 def visible_len(L: int, s_q: int, i: int, causal: bool) -> int:

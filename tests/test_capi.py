@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from mlc_decode_amd import _lib
-from mlc_decode_amd._lib import MlaDecodeArgs
+from mlc_decode_amd._lib import MlaDecodeArgs, MlaKvAppendArgs
 from mlc_decode_amd.api import get_mla_metadata_host
 from oracle import mla_ref as R
 
@@ -177,3 +177,46 @@ def test_python_api_refuses_cpu_tensors():
                                 torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32))
     with pytest.raises(ValueError):
         MlaKernel(1, 16, 2, 64)
+
+
+def _valid_append_args():
+    a = MlaKvAppendArgs()
+    a.batch, a.n_new, a.dtype, a.num_blocks = 2, 1, 0, 8
+    base = 1 << 20  # fake, aligned device addresses: validation fails before any use
+    a.kv_new = base
+    a.new_stride_b, a.new_stride_t = 576, 576
+    a.kv_nope, a.kv_rope = base, base + 1024
+    a.kv_stride_page = a.kv_rope_stride_page = 64 * 576
+    a.kv_stride_tok = a.kv_rope_stride_tok = 576
+    a.block_table, a.block_table_stride, a.max_pages = base, 4, 4
+    a.cache_seqlens = base
+    return a
+
+
+@pytest.mark.parametrize("field,value,needle", [
+    ("batch", 0, b"batch"),
+    ("n_new", 0, b"n_new"),
+    ("n_new", 65, b"n_new"),
+    ("dtype", 3, b"dtype"),
+    ("kv_new", None, b"NULL"),
+    ("cache_seqlens", None, b"NULL"),
+    ("kv_nope", (1 << 20) + 8, b"16-byte"),
+    ("new_stride_t", 580, b"strides"),
+    ("kv_stride_tok", -8, b"strides"),
+    ("max_pages", 0, b"max_pages"),
+    ("num_blocks", 0, b"num_blocks"),
+])
+def test_kv_append_rejects_bad_args(lib, field, value, needle):
+    a = _valid_append_args()
+    setattr(a, field, value)
+    rc = lib.mla_kv_append(ctypes.byref(a), None)
+    assert rc == 1
+    assert needle in lib.mla_last_error()
+
+
+def test_kv_append_python_checks():
+    from mlc_decode_amd import kv_append
+    new = torch.zeros(2, 1, 576, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):  # host tensors are refused: there is no CPU path
+        kv_append(new, torch.zeros(4, 64, 1, 576, dtype=torch.bfloat16),
+                  torch.zeros(2, 2, dtype=torch.int32), torch.zeros(2, dtype=torch.int32))

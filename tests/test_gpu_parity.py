@@ -13,7 +13,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from mlc_decode_amd import (MlaKernel, flash_mla_with_kvcache, get_mla_metadata,
+from mlc_decode_amd import (MlaKernel, flash_mla_with_kvcache, get_mla_metadata, kv_append,
                             get_mla_metadata_host, merge_partials, mla_decode_with_kvcache)
 from mlc_decode_amd.inputs import CONFIGS, MlaConfig, make_inputs
 from oracle import mla_ref as R
@@ -295,3 +295,65 @@ def test_benchmark_config(gpu, name):
     ref_o, ref_l = oracle_rows(inp, rows)
     idx = torch.tensor(rows)
     assert_parity(out.cpu()[idx], lse.cpu()[idx], ref_o, ref_l, name)
+
+
+# ---------------------------------------------------------------- paged KV-cache append
+def _append_inputs(seed, lens, n_new, P, dtype):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.tensor(lens, dtype=torch.int32)
+    B = len(lens)
+    N = B * P + 7
+    bt = torch.randperm(N, generator=g)[: B * P].to(torch.int32).view(B, P)
+    cache = torch.randn(N, 64, 1, 576, generator=g).to(dtype)
+    new = torch.randn(B, n_new, 576, generator=g).to(dtype)
+    return cache, bt, lens, new
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n_new", [1, 2, 3])
+def test_kv_append_matches_oracle(gpu, dtype, n_new):
+    """Bit-exact against the oracle, rows crossing page boundaries, one tensor or two views."""
+    cache, bt, lens, new = _append_inputs(40 + n_new, [0, 1, 62, 63, 64, 127, 200, 255], n_new, 5, dtype)
+    want_cache, want_lens, skipped = R.append_paged(cache, bt, lens, new)
+    assert skipped == []
+    for views in (False, True):
+        say(f"kv_append dtype={dtype} n_new={n_new} views={views}")
+        c = cache.to(gpu)
+        kvc = (c[..., :512], c[..., 512:]) if views else c
+        ln = lens.to(gpu)
+        st = torch.zeros(1, dtype=torch.int32, device=gpu)
+        kv_append(new.to(gpu), kvc, bt.to(gpu), ln, status=st)
+        torch.cuda.synchronize()
+        assert torch.equal(c.cpu(), want_cache)
+        assert torch.equal(ln.cpu(), want_lens)
+        assert st.item() == 0
+
+
+def test_kv_append_skips_unassigned_pages(gpu):
+    cache, bt, lens, new = _append_inputs(7, [10, 4 * 64 - 1, 64, 63, 5], 2, 4, torch.bfloat16)
+    bt[3, 1] = cache.shape[0]  # sequence 3 crosses into a page id past the cache
+    want_cache, want_lens, skipped = R.append_paged(cache, bt, lens, new)
+    assert skipped == [1, 3]
+    say("kv_append with unassigned pages")
+    c, ln = cache.to(gpu), lens.to(gpu)
+    st = torch.zeros(1, dtype=torch.int32, device=gpu)
+    kv_append(new.to(gpu), c, bt.to(gpu), ln, status=st)
+    torch.cuda.synchronize()
+    assert st.item() == 1
+    assert torch.equal(c.cpu(), want_cache) and torch.equal(ln.cpu(), want_lens)
+
+
+@pytest.mark.parametrize("H", [16, 128])
+def test_kv_append_then_decode(gpu, H):
+    """Decode over the appended cache matches the oracle decode of the extended sequences."""
+    cache, bt, lens, new = _append_inputs(11, [1, 63, 64, 300, 0], 1, 6, torch.bfloat16)
+    want_cache, want_lens, _ = R.append_paged(cache, bt, lens, new)
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(len(lens), 1, H, 576, generator=g).to(torch.bfloat16)
+    say(f"kv_append then decode H={H}")
+    c, ln, btg = cache.to(gpu), lens.to(gpu), bt.to(gpu)
+    kv_append(new.to(gpu), c, btg, ln)
+    out, lse = mla_decode_with_kvcache(q.to(gpu), c, btg, ln, sm_scale=576 ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    ref_o, ref_l = R.decode_paged(q, want_cache, bt, want_lens, 576 ** -0.5, True)
+    assert_parity(out, lse, ref_o, ref_l, f"append+decode H={H}")

@@ -271,3 +271,59 @@ def test_oracle_mistakes_are_caught():
             table[b, :n] = table[b, :n].flip(0)
     out, _ = R.decode_paged(c["q"], c["kv"], table, c["lengths"], SCALE, c["causal"])
     assert not torch.allclose(out, c["out"], atol=2e-5, rtol=1e-4)
+
+
+def _append_case(seed, B=6, n=2, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.tensor([0, 1, 62, 63, 64, 130][:B], dtype=torch.int32)
+    P = 4
+    N = B * P + 3
+    perm = torch.randperm(N, generator=g)[: B * P].to(torch.int32).view(B, P)
+    cache = torch.randn(N, R.PAGE, 1, R.D_QK, generator=g).to(dtype)
+    new = torch.randn(B, n, R.D_QK, generator=g).to(dtype)
+    return cache, perm, lens, new
+
+
+def test_append_oracle_against_gather():
+    """Appending then gathering a sequence gives its old tokens followed by the new ones, and
+    no other cache row changes."""
+    cache, bt, lens, new = _append_case(0)
+    out, lens2, skipped = R.append_paged(cache, bt, lens, new)
+    assert skipped == []
+    assert torch.equal(lens2, lens + new.shape[1])
+    written = torch.zeros(cache.shape[:2], dtype=torch.bool)
+    for b in range(len(lens)):
+        L, L2 = int(lens[b]), int(lens2[b])
+        got = R.gather(out[:, :, 0, :], bt[b], L2)
+        want = torch.cat([R.gather(cache[:, :, 0, :], bt[b], L), new[b]])
+        assert torch.equal(got, want)
+        for pos in range(L, L2):
+            written[int(bt[b, pos // R.PAGE]), pos % R.PAGE] = True
+    assert torch.equal(out[~written], cache[~written])
+
+
+def test_append_oracle_then_decode():
+    """Decoding the appended paged cache equals the contiguous closed form over the
+    concatenated tokens (the decode path consumes exactly what the append wrote)."""
+    cache, bt, lens, new = _append_case(1, n=1, dtype=torch.float32)
+    out, lens2, _ = R.append_paged(cache, bt, lens, new)
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(len(lens), 1, 16, R.D_QK, generator=g)
+    o_p, l_p = R.decode_paged(q, out, bt, lens2, R.D_QK ** -0.5, True)
+    for b in range(len(lens)):
+        kv = torch.cat([R.gather(cache[:, :, 0, :], bt[b], int(lens[b])), new[b]])
+        o_c = R.decode_contiguous(q[b:b + 1, 0, :, :512], q[b:b + 1, 0, :, 512:],
+                                  kv[None, :, None, :512], kv[None, :, None, 512:])
+        assert torch.allclose(o_p[b, 0], o_c[0], atol=1e-5, rtol=1e-5)
+
+
+def test_append_oracle_skips_unassigned_pages():
+    cache, bt, lens, new = _append_case(2, n=2)
+    bt = bt.clone()
+    lens = lens.clone()
+    lens[1] = 4 * R.PAGE - 1          # second token would need page slot 4 of a 4-slot table
+    bt[3, 1] = cache.shape[0]         # a page id past the cache, used by sequence 3 (63, 64)
+    out, lens2, skipped = R.append_paged(cache, bt, lens, new)
+    assert skipped == [1, 3]
+    assert lens2[1] == lens[1] and lens2[3] == lens[3]
+    assert lens2[0] == lens[0] + 2
