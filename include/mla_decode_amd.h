@@ -126,7 +126,10 @@ int mla_num_parts(int32_t batch, int32_t s_q, int32_t heads_q, int32_t heads_k, 
 
 /*
  * Kernel tile chosen for `rows` = s_q * heads_q query rows: waves per workgroup, 16-row tiles
- * per wave, LDS stages of 32 tokens in flight, rows per workgroup.  Returns 0, or
+ * per wave, LDS stages of 32 tokens in flight per ring, rows per workgroup.  When
+ * rows_per_workgroup is 16 * row_tiles (less than waves * 16 * row_tiles), the waves share one
+ * row tile and take turns over the KV stages, each with its own one-stage ring, and merge their
+ * results at the end of every segment.  Returns 0, or
  * MLA_ERR_INVALID for rows < 1 or a NULL output.  Replaces the block_H / threads / stages
  * fields of the tuned-config record (mla_best_configs.json:1-73).
  */

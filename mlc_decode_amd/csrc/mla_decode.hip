@@ -304,34 +304,40 @@ __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
 
-// Waves per SIMD a variant is compiled for: one 16-row tile per wave with at most a 2-stage
-// ring fits 256 registers, so two workgroups (or eight waves) share a CU; everything else
-// takes the whole register file (one wave per SIMD).
-constexpr int waves_per_simd(int nw, int ht, int nstage) {
-  return (ht == 1 && (nw == 8 || (nw == 4 && nstage <= 2))) ? 2 : 1;
+// Waves per SIMD a variant is compiled for: four waves of one 16-row tile each with at most
+// a 2-stage ring fit 256 registers, so two workgroups share a CU; everything else takes the
+// whole register file (one wave per SIMD).
+constexpr int waves_per_simd(int nw, int ht, int nstage, bool ws) {
+  return (!ws && ht == 1 && nw == 4 && nstage <= 2) ? 2 : 1;
 }
 
-template <int DT, int NW, int HT, int NSTAGE>
-__global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE) * 4 / NW > 0
-                                          ? waves_per_simd(NW, HT, NSTAGE) * 4 / NW : 1)
+// Two ways to use the NW waves of a workgroup:
+//  - WS = false: each wave owns its own 16*HT rows (R = NW*16*HT rows per workgroup) and all
+//    waves share one NSTAGE ring: every stage is loaded once, by all waves together, and
+//    consumed by all of them (a barrier per stage);
+//  - WS = true ("wave split", NSTAGE = 1): the waves share one 16*HT-row tile and take turns
+//    over the segment's stages (wave w takes stages w, w + NW, ...), each loading its own
+//    stages into its own one-stage slot with no barrier between waves; their accumulators are
+//    merged through LDS at the end of the segment, so the workgroup leaves one partial where
+//    NW single-wave workgroups would leave NW.
+template <int DT, int NW, int HT, int NSTAGE, bool WS>
+__global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW > 0
+                                          ? waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW : 1)
 void mla_splitkv_kernel(KParams p) {
-  // Stage loads are issued by the first NL waves (all of them up to four); with eight waves
-  // the other four only consume, and the per-stage barrier orders them after the loads.
-  constexpr int NL = NW < 4 ? NW : 4;
-  // With eight waves the second four run half a stage behind: each iteration they finish the
-  // previous stage's PV and then do this stage's QK, so on every SIMD one wave is reading K
-  // and issuing QK MFMAs while the other reads V^T for PV.  A lagging group still reads the
-  // previous stage's slot, so loads run LEAD = NSTAGE - 2 stages ahead instead of NSTAGE - 1.
-  constexpr bool kSkew = NW == 8;
-  constexpr int LEAD = kSkew ? NSTAGE - 2 : NSTAGE - 1;
-  static_assert(!kSkew || NSTAGE >= 3, "the skewed layout needs a ring of at least 3 stages");
+  static_assert(NW == 1 || NW == 4, "one or four waves per workgroup");
+  static_assert(!WS || NSTAGE == 1, "wave-split workgroups give each wave a one-stage slot");
+  constexpr int NL = WS ? 1 : NW;  // waves sharing the loads of one stage
+  constexpr int LEAD = NSTAGE - 1;
   static_assert((NSTAGE - 1) * (kLoadsPerStage / NL) < 64, "outstanding stage loads exceed vmcnt");
   static_assert(kLoadsPerStage % NL == 0, "loads per stage must split evenly");
-  constexpr int R = NW * 16 * HT;
+  constexpr int R = WS ? 16 * HT : NW * 16 * HT;
   constexpr int DK = 4;  // LDS prefetch depth of the QK A fragments
   constexpr int DV = HT == 2 ? 2 : 4;  // LDS prefetch depth of the PV A fragments
   constexpr float kTau = ref_tau<DT>();
-  __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[NSTAGE * kStageBytes];
+  constexpr int kSlots = WS ? NW : NSTAGE;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSlots * kStageBytes];
+  // wave-split merge words: (row max, row sum) per wave and row
+  __shared__ float merge_sh[WS ? NW : 1][2][16];
   // "score above reference" words, one per stage modulo 4.  A wave whose stage-k scores exceed
   // the reference stores 1 into over_sh[k % 4] (a wave-uniform branch, all lanes storing the
   // same value); every wave reads the word after the next barrier; wave 0 clears it two
@@ -347,7 +353,11 @@ void mla_splitkv_kernel(KParams p) {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;   // lane group (MFMA k quarter / output row quarter)
   const int li = lane & 15;  // lane within group
-  const int row0 = hb * R + wave * 16 * HT;
+  const int row0 = hb * R + (WS ? 0 : wave * 16 * HT);
+  // this wave's stage ring, and the first stage / stride of its turn over a segment
+  uint8_t LDS_AS* const ring = smem + (WS ? wave * kStageBytes : 0);
+  const int k0 = WS ? wave : 0;
+  constexpr int kStep = WS ? NW : 1;
 
   const int32_t* rec = p.sched + part * kSchedWords;
   int b = rec[0];
@@ -437,9 +447,8 @@ void mla_splitkv_kernel(KParams p) {
         rb = p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st);
       }
       const int left = L - st * kStageTok;
-      if (wave < NL)  // uniform
-        issue_stage<NL>(smem + (k % NSTAGE) * kStageBytes, nb, rb, kv_st, kr_st,
-                        (left < kStageTok ? left : kStageTok) - 1, wave, lane);
+      issue_stage<NL>(ring + (k % NSTAGE) * kStageBytes, nb, rb, kv_st, kr_st,
+                      (left < kStageTok ? left : kStageTok) - 1, NL == 1 ? 0 : wave, lane);
     };
 
     // One pass over the segment's stages.  Returns true (uniformly across the workgroup)
@@ -458,7 +467,7 @@ void mla_splitkv_kernel(KParams p) {
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) m_ref[ht] = -INFINITY;
       }
-      if constexpr (MODE == kPassFirstStageRef) {
+      if constexpr (MODE == kPassFirstStageRef && !WS) {
         if (wave == 0) over_sh[lane & 3] = 0;  // uniform branch; ordered by the first barriers
         wait_lgkm0();
       }
@@ -466,25 +475,25 @@ void mla_splitkv_kernel(KParams p) {
       wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
 
       if constexpr (NSTAGE == 1) {
-        if (nst > 0) issue(0);
+        if (k0 < nst) issue(k0);
       } else {
 #pragma unroll
         for (int k = 0; k < LEAD; ++k)
           if (k < nst) issue(k);
       }
-      // One LDS buffer (NSTAGE == 1): the next stage is loaded into it once every wave of
-      // the workgroup has consumed the current one; latency is hidden by the other
-      // workgroups sharing the CU instead.
+      // One LDS buffer (NSTAGE == 1): the next stage is loaded into it once every wave
+      // sharing it has consumed the current one; latency is hidden by the other waves of the
+      // CU instead.
       auto refill_single = [&](int k) __attribute__((always_inline)) {
         if constexpr (NSTAGE == 1) {
-          if constexpr (NW > 1) lds_barrier();
-          if (k + 1 < nst) issue(k + 1);
+          if constexpr (NW > 1 && !WS) lds_barrier();
+          if (k + kStep < nst) issue(k + kStep);
         }
       };
 
       // ---- O^T += V^T P^T over the 32 tokens of stage kp; DV fragments in flight
       auto v_base = [&](int kp) __attribute__((always_inline)) {
-        const uint8_t LDS_AS* vb = smem + (kp % NSTAGE) * kStageBytes + v_lane;
+        const uint8_t LDS_AS* vb = ring + (kp % NSTAGE) * kStageBytes + v_lane;
         asm volatile("" : "+v"(vb));
         return vb;
       };
@@ -513,35 +522,30 @@ void mla_splitkv_kernel(KParams p) {
         // write to their registers can be placed before it.
         operand_guard<HT>(pb, vf[(kDimTiles - 1) % DV]);
       };
-      const bool lagging = kSkew && wave >= NW / 2;  // uniform
-      i32x4 pb_lag[HT];
-
       bool abort = false;
+      // wave-split: this wave's own "score above reference" flag of its previous stage
+      bool over_prev = false;
 #pragma unroll 1
-      for (int k = 0; k < nst; ++k) {
+      for (int j = 0, k = k0; k < nst; ++j, k += kStep) {  // j: the wave's own stage count
         const int remaining_after = nst - 1 - k;
-        if (wave < NL)  // uniform
-          wait_stage<NL, NSTAGE>(remaining_after < LEAD - 1 ? remaining_after : LEAD - 1);
-        lds_barrier();
+        wait_stage<NL, NSTAGE>(remaining_after < LEAD - 1 ? remaining_after : LEAD - 1);
+        if constexpr (!WS) lds_barrier();
         // the previous stage's flags, read now and tested after this stage's QK product
         int prev_over = 0;
         if constexpr (MODE == kPassFirstStageRef) {
-          if (k > 0) prev_over = over_sh[(k - 1) & 3];
-          if (k > 1 && wave == 0) over_sh[(k - 2) & 3] = 0;  // uniform branch
+          if constexpr (WS) {
+            prev_over = over_prev;
+          } else {
+            if (k > 0) prev_over = over_sh[(k - 1) & 3];
+            if (k > 1 && wave == 0) over_sh[(k - 2) & 3] = 0;  // uniform branch
+          }
         }
         if constexpr (NSTAGE > 1) {
           if (k + LEAD < nst) issue(k + LEAD);
         }
 
-        const uint8_t LDS_AS* sb = smem + (k % NSTAGE) * kStageBytes;
+        const uint8_t LDS_AS* sb = ring + (k % NSTAGE) * kStageBytes;
         const int st = st_begin + k;
-        if constexpr (kSkew && MODE != kPassRowMax) {
-          if (lagging && k > 0) {
-            i32x4 vfl[DV];
-            v_prefetch(k - 1, vfl);
-            pv_stage(k - 1, pb_lag, vfl);
-          }
-        }
 
         // ---- S^T = K Q^T over 576 dims: two 16-token tiles x HT 16-row tiles.
         // Fragment n = 2*kk + tt; DK fragments in flight ahead of the MFMAs.
@@ -585,7 +589,7 @@ void mla_splitkv_kernel(KParams p) {
         }
         i32x4 vf[DV];
         if constexpr (MODE != kPassRowMax) {
-          if (!(kSkew && lagging)) v_prefetch(k, vf);
+          v_prefetch(k, vf);
         }
 
         // ---- mask tokens past each row's limit (sequence tail / causal)
@@ -621,14 +625,18 @@ void mla_splitkv_kernel(KParams p) {
           continue;
         }
         if constexpr (MODE == kPassFirstStageRef) {
-          if (k == 0) {
+          if (WS ? j == 0 : k == 0) {
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) m_ref[ht] = wave_max_g(lmx[ht]);
           } else {
             bool over = false;
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
-            if (__builtin_amdgcn_ballot_w64(over) != 0) over_sh[k & 3] = 1;  // uniform branch
+            if constexpr (WS) {
+              over_prev = __builtin_amdgcn_ballot_w64(over) != 0;
+            } else {
+              if (__builtin_amdgcn_ballot_w64(over) != 0) over_sh[k & 3] = 1;  // uniform branch
+            }
           }
         }
 
@@ -648,34 +656,24 @@ void mla_splitkv_kernel(KParams p) {
                          (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
         }
 
-        if constexpr (kSkew) {
-          if (lagging) {
-#pragma unroll
-            for (int ht = 0; ht < HT; ++ht) pb_lag[ht] = pb[ht];
-          } else {
-            pv_stage(k, pb, vf);
-          }
-        } else {
-          pv_stage(k, pb, vf);
-        }
+        pv_stage(k, pb, vf);
         refill_single(k);
-        if constexpr (MODE == kPassFirstStageRef) wait_lgkm0();  // flag store lands before the barrier
-      }
-      if constexpr (kSkew && MODE != kPassRowMax) {
-        if (lagging && !abort && nst > 0) {
-          i32x4 vfl[DV];
-          v_prefetch(nst - 1, vfl);
-          pv_stage(nst - 1, pb_lag, vfl);
-        }
+        if constexpr (MODE == kPassFirstStageRef && !WS) wait_lgkm0();  // flag store lands before the barrier
       }
       if constexpr (MODE == kPassFirstStageRef) {
-        if (!abort && nst > 1) {  // the last stage's flags
-          lds_barrier();
-          abort = over_sh[(nst - 1) & 3] != 0;
+        if constexpr (WS) {
+          if (!abort) abort = over_prev;  // the wave's last stage's flag
+        } else {
+          if (!abort && nst > 1) {  // the last stage's flags
+            lds_barrier();
+            abort = over_sh[(nst - 1) & 3] != 0;
+          }
         }
       }
       wait_vmcnt<0>();  // an abandoned pass may leave stage loads in flight
-      lds_barrier();    // every wave is done with the LDS ring before it is refilled
+      // every wave is done with the LDS ring before it is refilled (a wave-split slot has one
+      // user)
+      if constexpr (!WS) lds_barrier();
       return abort;
     };
 
@@ -695,6 +693,92 @@ void mla_splitkv_kernel(KParams p) {
     // its lse (the same value).
     const int slot0 = p.splits[b];
     const bool single = (p.splits[b + 1] - slot0) == 1;
+    if constexpr (WS) {
+      // ---- wave-split merge.  Wave w holds (m_w, l_w, O_w) over its stages (m_w = -inf and
+      // l_w = 0 for a wave that had none); the segment's result is
+      //   O = sum_w 2^(m_w - m) O_w / lsum,  lsum = sum_w 2^(m_w - m) l_w,  m = max_w m_w,
+      // and lse = m + log2(lsum) (log2 units, as every split's lse).  Each wave scales its O_w
+      // into LDS (fp32 rows of 512 with a 16-byte pad: conflict-free 16-byte stores), then
+      // wave w sums and stores dims 128w .. 128w + 127 of all 16 rows.  The slots are free:
+      // every wave waited for its own stage loads before the first barrier.
+      constexpr int kMergePitch = kDV * 4 + 16;
+      static_assert(NW * 16 * kMergePitch <= kSlots * kStageBytes, "merge staging exceeds the slots");
+      const int64_t slot = slot0 + split;
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        const float l_w = wave_sum_g(l_part[ht]);
+        if (g == 0) {
+          merge_sh[wave][0][li] = m_ref[ht];
+          merge_sh[wave][1][li] = l_w;
+        }
+        wait_lgkm0();
+        lds_barrier();
+        float m = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) m = fmaxf(m, merge_sh[v][0][li]);
+        float lsum = 0.f, c = 0.f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) {
+          const float mv = merge_sh[v][0][li];
+          const float sv = mv == -INFINITY ? 0.f : fast_exp2(mv - m);
+          lsum += sv * merge_sh[v][1][li];
+          if (v == wave) c = sv;  // uniform
+        }
+        c *= lsum > 0.f ? 1.f / lsum : 0.f;
+        uint8_t LDS_AS* mine = smem + (wave * 16 + li) * kMergePitch + 16 * g;
+#pragma unroll
+        for (int dt = 0; dt < kDimTiles; ++dt) {  // O_w^T tile dt: row li, dims 16dt + 4g ..
+          *(f32x4 LDS_AS*)(mine + 64 * dt) = o[dt][ht] * c;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        wait_lgkm0();
+        lds_barrier();
+        // lane (q, cc) = (lane / 16, lane % 16): rows q, q + 4, q + 8, q + 12, dims
+        // 128w + 4cc .. + 3 and 128w + 64 + 4cc .. + 3 (16 lanes read 256 contiguous bytes:
+        // conflict-free).  Padding rows store the last row's (identical) values.
+        const int cc = lane & 15, q = lane >> 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = q + 4 * i;
+          f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
+#pragma unroll
+          for (int v = 0; v < NW; ++v) {
+            const uint8_t LDS_AS* src = smem + (v * 16 + r) * kMergePitch + (128 * wave + 4 * cc) * 4;
+            a0 += *(const f32x4 LDS_AS*)src;
+            a1 += *(const f32x4 LDS_AS*)(src + 256);
+          }
+          int row = row0 + 16 * ht + r;
+          row = row < p.rows ? row : p.rows - 1;
+          const i32x2 lo = i32x2{(int)pack2<DT>(a0[0], a0[1]), (int)pack2<DT>(a0[2], a0[3])};
+          const i32x2 hi = i32x2{(int)pack2<DT>(a1[0], a1[1]), (int)pack2<DT>(a1[2], a1[3])};
+          uint16_t* d;
+          if (single) {  // uniform
+            const int s = row / p.heads;
+            const int h = row - s * p.heads;
+            d = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh);
+          } else {
+            d = p.ws_o + (slot * p.rows + row) * kDV;
+          }
+          d += 128 * wave + 4 * cc;
+          *(i32x2*)d = lo;
+          *(i32x2*)(d + 64) = hi;
+        }
+        if (wave == 0) {  // uniform: the four lane groups of a row store the same lse
+          int row = row0 + 16 * ht + li;
+          row = row < p.rows ? row : p.rows - 1;
+          const float lse2 = lsum > 0.f ? m + __log2f(lsum) : -INFINITY;
+          const int s = row / p.heads;
+          const int h = row - s * p.heads;
+          if (single) {
+            if (p.lse != nullptr) p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
+          } else {
+            p.ws_lse[slot * p.rows + row] = lse2;
+          }
+        }
+        lds_barrier();  // staging and merge words are read before their next use
+      }
+      continue;
+    }
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
       const float l = wave_sum_g(l_part[ht]);
@@ -1002,29 +1086,38 @@ int fail(int code, const std::string& msg) {
 
 struct Variant {
   int nw, ht, nstage;
+  bool ws;  // wave split: the waves share one row tile and take turns over the stages
+  int rows() const { return ws ? 16 * ht : nw * 16 * ht; }
+  int lds() const { return (ws ? nw : nstage) * mla::kStageBytes; }
 };
 
-// Rows per workgroup R = nw*16*ht; LDS per workgroup nstage*36 KiB.  A wave owns one 16-row
-// tile (72 VGPRs of query, 128 AGPRs of fp32 output) or two (32 rows: 144 VGPRs of query,
-// 256 AGPRs of output, and every K / V fragment read from LDS feeds two MFMAs).
-//  - up to 32 rows: one wave per workgroup with a single 36 KiB stage buffer, four
-//    workgroups per CU; each waits for its own stage while the others compute, which keeps
-//    4 x 36 KiB of loads in flight per CU (one wave alone could hold at most 63 KiB: vmcnt);
-//  - up to 64 rows: four waves of one tile sharing a 4-stage ring;
+// A wave owns one 16-row tile (72 VGPRs of query, 128 AGPRs of fp32 output) or two (32 rows:
+// 144 VGPRs of query, 256 AGPRs of output, and every K / V fragment read from LDS feeds two
+// MFMAs).
+//  - up to 16 rows: four waves take turns over the stages of one tile, each with its own
+//    36 KiB slot (one workgroup per CU).  Each wave waits for its own stage while the others
+//    compute, which keeps 4 x 36 KiB of loads in flight per CU (one wave alone could hold at
+//    most 63 KiB: vmcnt), and the merge at the end of a segment leaves one partial per
+//    workgroup instead of one per wave: a quarter of the split partials (their stores cost
+//    far more than their bytes suggest when they interleave with the KV reads) and a quarter
+//    of the page-granular imbalance between parts;
+//  - up to 32 rows: one wave of two tiles per workgroup with its own 36 KiB stage buffer,
+//    four workgroups per CU (the wave-split form of two tiles spills registers);
+//  - up to 64 rows: four waves of one tile each sharing a 4-stage ring;
 //  - above 64 rows: four waves of two tiles (128 rows) sharing a 3-stage ring, so each KV
 //    stage is read into LDS once for all 128 rows; more rows use ceil(rows/128) head blocks.
 Variant pick_variant(int rows) {
-  if (rows <= 16) return {1, 1, 1};
-  if (rows <= 32) return {1, 2, 1};
-  if (rows <= 64) return {4, 1, 4};
-  return {4, 2, 3};
+  if (rows <= 16) return {4, 1, 1, true};
+  if (rows <= 32) return {1, 2, 1, false};
+  if (rows <= 64) return {4, 1, 4, false};
+  return {4, 2, 3, false};
 }
 
 int wgs_per_cu(const Variant& v) {
-  const int lds = v.nstage * mla::kStageBytes;
+  const int lds = v.lds();
   int by_lds = (160 * 1024) / lds;
   if (by_lds < 1) by_lds = 1;
-  const int per_simd = mla::waves_per_simd(v.nw, v.ht, v.nstage);
+  const int per_simd = mla::waves_per_simd(v.nw, v.ht, v.nstage, v.ws);
   const int by_waves = 4 * per_simd / v.nw > 0 ? 4 * per_simd / v.nw : 1;
   return by_lds < by_waves ? by_lds : by_waves;
 }
@@ -1047,21 +1140,19 @@ int64_t ws_lse_bytes(int64_t slots, int64_t rows) {
   return ((slots * rows * 4) + 255) / 256 * 256;
 }
 
-template <int DT, int NW, int HT, int NS>
+template <int DT, int NW, int HT, int NS, bool WS>
 hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) {
-  hipLaunchKernelGGL((mla::mla_splitkv_kernel<DT, NW, HT, NS>), dim3(kp.num_parts, head_blocks),
+  hipLaunchKernelGGL((mla::mla_splitkv_kernel<DT, NW, HT, NS, WS>), dim3(kp.num_parts, head_blocks),
                      dim3(NW * 64), 0, st, kp);
   return hipGetLastError();
 }
 
 template <int DT>
 hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blocks, hipStream_t st) {
-  if (v.nw == 1) {
-    if (v.ht == 1) return launch_main<DT, 1, 1, 1>(kp, head_blocks, st);
-    return launch_main<DT, 1, 2, 1>(kp, head_blocks, st);
-  }
-  if (v.ht == 1) return launch_main<DT, 4, 1, 4>(kp, head_blocks, st);
-  return launch_main<DT, 4, 2, 3>(kp, head_blocks, st);
+  if (v.ws) return launch_main<DT, 4, 1, 1, true>(kp, head_blocks, st);
+  if (v.nw == 1) return launch_main<DT, 1, 2, 1, false>(kp, head_blocks, st);
+  if (v.ht == 1) return launch_main<DT, 4, 1, 4, false>(kp, head_blocks, st);
+  return launch_main<DT, 4, 2, 3, false>(kp, head_blocks, st);
 }
 
 int validate(const mla_decode_args* a, int64_t* need_ws) {
@@ -1175,7 +1266,7 @@ int mla_variant(int32_t rows, int32_t* waves, int32_t* row_tiles, int32_t* stage
   *waves = v.nw;
   *row_tiles = v.ht;
   *stages = v.nstage;
-  *rows_per_workgroup = v.nw * 16 * v.ht;
+  *rows_per_workgroup = v.rows();
   return MLA_OK;
 }
 
@@ -1186,7 +1277,7 @@ int mla_num_parts(int32_t batch, int32_t s_q, int32_t heads_q, int32_t heads_k, 
   }
   const int rows = s_q * heads_q;
   const Variant v = pick_variant(rows);
-  const int R = v.nw * 16 * v.ht;
+  const int R = v.rows();
   const int head_blocks = (rows + R - 1) / R;
   const int cus = cu_count > 0 ? cu_count : cu_count_current();
   int parts = cus * wgs_per_cu(v) / head_blocks;
@@ -1253,7 +1344,7 @@ int mla_splitkv_fwd(const mla_decode_args* args, void* stream) {
   if (rc != MLA_OK) return rc;
   const mla::KParams kp = make_params(args);
   const Variant v = pick_variant(kp.rows);
-  const int R = v.nw * 16 * v.ht;
+  const int R = v.rows();
   const int head_blocks = (kp.rows + R - 1) / R;
   const hipError_t e = args->dtype == MLA_DTYPE_BF16
                            ? launch_main_dt<MLA_DTYPE_BF16>(v, kp, head_blocks, (hipStream_t)stream)

@@ -91,9 +91,10 @@ def test_workspace_bytes(lib):
 
 
 def test_num_parts(lib):
-    # up to 32 rows: four single-wave workgroups per CU; up to 64 rows: one 64-row workgroup
-    # per CU; above: one 128-row workgroup per CU, head blocks sharing the CU count
-    assert lib.mla_num_parts(1, 1, 16, 1, 256) == 1024
+    # up to 16 rows: one workgroup per CU whose four waves share one tile; up to 32 rows: four
+    # single-wave workgroups per CU; up to 64 rows: one 64-row workgroup per CU; above: one
+    # 128-row workgroup per CU, head blocks sharing the CU count
+    assert lib.mla_num_parts(1, 1, 16, 1, 256) == 256
     assert lib.mla_num_parts(1, 1, 32, 1, 256) == 1024
     assert lib.mla_num_parts(1, 1, 64, 1, 256) == 256
     assert lib.mla_num_parts(64, 1, 128, 1, 256) == 256
@@ -105,7 +106,7 @@ def test_num_parts(lib):
 def test_variant_query(lib):
     vals = [ctypes.c_int32() for _ in range(4)]
     ptrs = [ctypes.byref(v) for v in vals]
-    assert lib.mla_variant(16, *ptrs) == 0 and [v.value for v in vals] == [1, 1, 1, 16]
+    assert lib.mla_variant(16, *ptrs) == 0 and [v.value for v in vals] == [4, 1, 1, 16]
     assert lib.mla_variant(32, *ptrs) == 0 and [v.value for v in vals] == [1, 2, 1, 32]
     assert lib.mla_variant(64, *ptrs) == 0 and [v.value for v in vals] == [4, 1, 4, 64]
     assert lib.mla_variant(128, *ptrs) == 0 and [v.value for v in vals] == [4, 2, 3, 128]
