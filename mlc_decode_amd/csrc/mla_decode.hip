@@ -196,7 +196,7 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
   const uint64_t sbase = ((uint64_t)hi << 32) | (uint64_t)lo;
   asm volatile(
       "s_mov_b32 m0, %2\n\t"
-      "global_load_lds_dwordx4 %0, %1"
+      "global_load_lds_dwordx4 %0, %1 nt"
       :
       : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
       : "memory", "m0");
@@ -228,34 +228,39 @@ __device__ __forceinline__ float wave_sum_g(float v) {
 // ---------------------------------------------------------------------------------------
 // stage loads: HBM -> LDS, 36 wave-wide 16-byte loads per 32-token stage
 // ---------------------------------------------------------------------------------------
-// LDS layout of a stage: two panels of 16 token rows; inside a panel the 16-byte chunk c
-// (dims 8c..8c+7) of row r sits at slot c*16 + (r ^ 8*(c&1)), i.e.
-//   byte(c, r) = ((r/16)*72*16 + c*16 + ((r%16) ^ ((c&1) << 3))) * 16.
-// Load i (one wave-wide global_load_lds_dwordx4 = 1 KiB) fills panel i/18, chunks
-// 4*(i%18) .. +3: lane l fetches chunk 4*(i%18) + l/16 of panel row (l%16) ^ 8*((l/16)&1),
-// so each lane's source is one per-stage base plus an immediate, and every token row
-// contributes 64 contiguous bytes per load.  Loads with i%18 >= 16 fetch the rope dims.
-template <int NW>
+// LDS layout of a stage (32 token rows of 72 16-byte chunks): 36 blocks of 1 KiB.  Block
+// q*9 + s (q = 0..3) holds token rows 8q .. 8q+7 (row group q: panel q/2, half q%2) and
+// chunks 8s .. 8s+7 (s = 8: the rope dims); inside a block, chunk 8s + c8 of row r sits at
+// 16-byte slot 8*(r%8) + (c8 ^ swz(r % 16)), with
+//   swz(r) = 2*((r/2) % 4) + r/8.
+// One wave-wide global_load_lds_dwordx4 fills one block: lane l fetches row 8q + l/8, chunk
+// 8s + ((l%8) ^ swz), so the eight lanes of a row cover one whole 128-byte line and every
+// load reads eight full lines (which the non-temporal policy streams at ~15% more bandwidth
+// than half-line accesses; half lines under that policy are fetched twice).  The swizzle
+// keeps the fragment reads conflict-free: the sixteen rows of one chunk (QK A operand) and
+// the 4-row x 2-chunk V^T blocks of one transposed read spread over all 64 banks.
+__device__ __forceinline__ int stage_swz(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
+
+template <int NL>
 __device__ __forceinline__ void issue_stage(uint8_t LDS_AS* slot, const uint16_t* nope_base,
                                             const uint16_t* rope_base, int kv_st, int kr_st,
                                             int last_row, int wave, int lane) {
-  const int prow = (lane & 15) ^ (((lane >> 4) & 1) << 3);
-  const uint32_t cl = (uint32_t)(lane >> 4) * 16;  // byte offset of the lane's chunk in a load
-  // Rows past the sequence end re-read its last row: in bounds, finite, masked later.
-  const int r0 = prow < last_row ? prow : last_row;
-  const int r1 = prow + 16 < last_row ? prow + 16 : last_row;
-  const uint32_t on0 = (uint32_t)(r0 * kv_st) * 2 + cl, on1 = (uint32_t)(r1 * kv_st) * 2 + cl;
-  const uint32_t or0 = (uint32_t)(r0 * kr_st) * 2 + cl, or1 = (uint32_t)(r1 * kr_st) * 2 + cl;
+  // NL = 4: wave w loads row group w (9 blocks); NL = 1: the wave loads all 36 blocks.
+  static_assert(NL == 1 || NL == 4, "stage loads are split over one or four waves");
 #pragma unroll
-  for (int j = 0; j < kLoadsPerStage / NW; ++j) {
-    const int i = wave + NW * j;  // wave is uniform, so the panel / rope choice is scalar
-    const int panel = i >= 18;
-    const int ii = i - 18 * panel;
-    if (ii < 16)
-      dma16((const char*)nope_base + 64 * ii, panel ? on1 : on0, (uint32_t)(uintptr_t)(slot + i * 1024));
-    else
-      dma16((const char*)rope_base + 64 * (ii - 16), panel ? or1 : or0,
-            (uint32_t)(uintptr_t)(slot + i * 1024));
+  for (int qi = 0; qi < 4 / NL; ++qi) {
+    const int q = NL == 1 ? qi : wave;  // uniform
+    // Rows past the sequence end re-read its last row: in bounds, finite, masked later.
+    int row = 8 * q + (lane >> 3);
+    row = row < last_row ? row : last_row;
+    const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((q & 1) << 3) | (lane >> 3))) << 4);
+    const uint32_t on = (uint32_t)(row * kv_st) * 2 + cl;
+    const uint32_t orp = (uint32_t)(row * kr_st) * 2 + cl;
+    uint8_t LDS_AS* dst = slot + q * 9 * 1024;
+#pragma unroll
+    for (int sg = 0; sg < 8; ++sg)
+      dma16((const char*)nope_base + 128 * sg, on, (uint32_t)(uintptr_t)(dst + sg * 1024));
+    dma16(rope_base, orp, (uint32_t)(uintptr_t)(dst + 8 * 1024));
   }
 }
 
@@ -366,17 +371,19 @@ void mla_splitkv_kernel(KParams p) {
   const int end_page = rec[3];
   int split = rec[4];
 
-  // Per-lane LDS byte offsets that do not depend on the stage (panel layout above).
+  // Per-lane LDS byte offsets that do not depend on the stage (block layout above).
   // QK A operand, fragment (kk, tt): token row 16*tt + li of chunk sigma(kk, g), where
-  //   sigma(kk, g) = 8*(kk/2) + 2*g + kk%2
-  // permutes the contraction order so that the four lane groups of one read see chunks of
-  // the same parity: the row XOR (8 on odd chunks) is then uniform across the read, which
-  // ds_read_b128 needs to stay conflict-free (the query fragments use the same sigma).
-  const int k_lane0 = (2 * g) * 256 + (li << 4);
-  const int k_lane1 = (2 * g + 1) * 256 + ((li ^ 8) << 4);
-  // V^T A operand, dim tile dt: the lane addresses token row 4g + li/4 (and the same row of
-  // the second panel), bytes 32*dt + 8*(li%4), i.e. chunk 2*dt + (li%4)/2.
-  const int v_lane = ((li >> 1) & 1) * 256 + (((4 * g + (li >> 2)) ^ (((li >> 1) & 1) << 3)) << 4) +
+  //   sigma(kk, g) = 8*(kk/2) + 2*g + kk%2,
+  // i.e. block (2tt + li/8)*9 + kk/2, chunk-in-block 2g + kk%2: one lane offset per parity of
+  // kk, the rest (tt, kk/2) an immediate.  The query fragments use the same sigma.
+  const int k_lane0 = (li >> 3) * 9216 + ((((li & 7) << 3) + ((2 * g) ^ stage_swz(li))) << 4);
+  const int k_lane1 = (li >> 3) * 9216 + ((((li & 7) << 3) + ((2 * g + 1) ^ stage_swz(li))) << 4);
+  // V^T A operand, dim tile dt = 4s + d4: the lane addresses token row rv = 4g + li/4 (and the
+  // same row of the second panel), bytes 32*dt + 8*(li%4), i.e. chunk 8s + 2*d4 + (li%4)/2 in
+  // block (rv/8)*9 + s.  The chunk's swizzle only flips bits 5-6 of the address with d4, so the
+  // address of tile dt is (v_lane ^ 32*d4) + 1024*s over a 1 KiB-aligned stage base.
+  const int rv = 4 * g + (li >> 2);
+  const int v_lane = (rv >> 3) * 9216 + ((rv & 7) << 7) + (((li >> 1) & 1) ^ stage_swz(rv)) * 16 +
                      ((li & 1) << 3);
 
   const int kv_st = (int)p.kv_st, kr_st = (int)p.kr_st;
@@ -497,24 +504,30 @@ void mla_splitkv_kernel(KParams p) {
         asm volatile("" : "+v"(vb));
         return vb;
       };
+      // Tiles go in d4-major order, t = 8*d4 + s for dim tile dt = 4s + d4, so the XOR of the
+      // lane address changes once per eight tiles.
+      auto v_frag = [&](const uint8_t LDS_AS* vb, int t) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* xb =
+            (t >> 3) ? (const uint8_t LDS_AS*)(uintptr_t)((uint32_t)(uintptr_t)vb ^ (uint32_t)(32 * (t >> 3))) : vb;
+        return lds_tr_pair(xb + (t & 7) * 1024);
+      };
       // the first DV V^T fragments of stage kp (issued ahead of the softmax to hide latency)
       auto v_prefetch = [&](int kp, i32x4 (&vf)[DV]) __attribute__((always_inline)) {
         const uint8_t LDS_AS* vb = v_base(kp);
 #pragma unroll
-        for (int n = 0; n < DV; ++n) vf[n] = lds_tr_pair(vb + n * 512);
+        for (int n = 0; n < DV; ++n) vf[n] = v_frag(vb, n);
       };
       auto pv_stage = [&](int kp, i32x4 (&pb)[HT], i32x4 (&vf)[DV]) __attribute__((always_inline)) {
         const uint8_t LDS_AS* vb = v_base(kp);
-#define MLA_VFRAG(DTI) lds_tr_pair(vb + (DTI) * 512)
 #pragma unroll
-        for (int dt = 0; dt < kDimTiles; ++dt) {
-          const i32x4 a = vf[dt % DV];
-          if (dt + DV < kDimTiles) vf[dt % DV] = MLA_VFRAG(dt + DV);
+        for (int t = 0; t < kDimTiles; ++t) {
+          const int dt = 4 * (t & 7) + (t >> 3);
+          const i32x4 a = vf[t % DV];
+          if (t + DV < kDimTiles) vf[t % DV] = v_frag(vb, t + DV);
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) o[dt][ht] = mfma32<DT>(a, pb[ht], o[dt][ht]);
           __builtin_amdgcn_sched_barrier(0);
         }
-#undef MLA_VFRAG
         // The last MFMAs are still reading their A/B operands (P^T and the last V^T fragment)
         // over several passes after they issue.  The compiler's hazard model lets a VALU write
         // reuse those registers a few cycles later (seen corrupting the last dim tile of the
@@ -558,7 +571,7 @@ void mla_splitkv_kernel(KParams p) {
         asm volatile("" : "+v"(kb0));
         asm volatile("" : "+v"(kb1));
 #define MLA_KFRAG(N) \
-  (*(const i32x4 LDS_AS*)((((N) >> 1) & 1 ? kb1 : kb0) + ((N) & 1) * kPanelBytes + ((N) >> 2) * 2048))
+  (*(const i32x4 LDS_AS*)((((N) >> 1) & 1 ? kb1 : kb0) + ((N) & 1) * kPanelBytes + ((N) >> 2) * 1024))
 #pragma unroll
         for (int n = 0; n < DK; ++n) kf[n] = MLA_KFRAG(n);
 #pragma unroll
