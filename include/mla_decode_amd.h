@@ -55,6 +55,10 @@ extern "C" {
 /* Per-split overhead, in pages, of the default (min-payload) tile schedule. */
 #define MLA_DEFAULT_SPLIT_OVERHEAD 3
 
+/* KV cache formats (mla_decode_args.kv_format, mla_kv_append_args.kv_format). */
+#define MLA_KV_NATIVE 0   /* latent and rope in the query dtype */
+#define MLA_KV_FP8_E4M3 1 /* latent as OCP e4m3 codes with power-of-two scales (below) */
+
 /*
  * Decode arguments.  Strides are in elements.  The latent ("nope", dims
  * 0..511) and rope (dims 512..575) halves may live in one tensor (rope pointer
@@ -75,6 +79,16 @@ extern "C" {
  * out element (b, s, h, d) is at out + b*o_stride_b + s*o_stride_s + h*o_stride_h + d.
  * lse is a contiguous fp32 [B, H, s_q] array (natural log of the softmax denominator
  * of sm_scale * q.k); rows with no visible key get out = 0 and lse = -inf.
+ *
+ * kv_format == MLA_KV_FP8_E4M3 (paged only, dtype bf16): kv_nope points to uint8 OCP e4m3
+ * codes (strides in bytes: 16-byte multiples; a token's 512 codes contiguous); kv_rope holds
+ * the rope dims in bf16 as above; kv_scale holds fp32 scales, the scale of token row r of
+ * page p and 128-dim block j (dims 128j .. 128j+127) at
+ *   kv_scale + p*kv_scale_stride_page + j*kv_scale_stride_blk + r
+ * (strides in floats, multiples of 4, pointer 16-byte aligned).  Latent value d of a token is
+ * e4m3(code_d) * scale_{d/128}; every scale must be a power of two (2^-126 .. 2^127), as
+ * mla_kv_append writes them: the device applies it as an exponent.  The rope and the
+ * queries are bf16.  With MLA_KV_NATIVE, kv_scale is unused and may be NULL.
  */
 typedef struct mla_decode_args {
   int32_t batch;
@@ -109,6 +123,11 @@ typedef struct mla_decode_args {
 
   void* workspace;
   int64_t workspace_bytes;
+
+  int32_t kv_format;   /* MLA_KV_NATIVE or MLA_KV_FP8_E4M3 */
+  int32_t kv_reserved; /* must be 0 */
+  const float* kv_scale;
+  int64_t kv_scale_stride_page, kv_scale_stride_blk;
 } mla_decode_args;
 
 /* Library version (MLA_DECODE_AMD_VERSION). */
@@ -254,6 +273,15 @@ typedef struct mla_kv_append_args {
   int32_t max_pages;
   int32_t* cache_seqlens;     /* [B], advanced in place */
   int32_t* status;            /* optional device word, set to 1 on a skipped sequence */
+  /* MLA_KV_FP8_E4M3: the cache is in the fp8 format of mla_decode_args (kv_nope = e4m3
+   * codes, kv_scale = power-of-two scales, kv_rope bf16); kv_new stays bf16 and each new
+   * token's latent block j is stored as e4m3(x / 2^k) with 2^k the smallest power of two
+   * such that max|x| over the block <= 448 * 2^k (k clamped to [-126, 127]; a zero block
+   * gets k = 0), rounded to nearest even. */
+  int32_t kv_format;
+  int32_t kv_reserved; /* must be 0 */
+  float* kv_scale;
+  int64_t kv_scale_stride_page, kv_scale_stride_blk;
 } mla_kv_append_args;
 
 int mla_kv_append(const mla_kv_append_args* args, void* stream);

@@ -16,6 +16,8 @@ MLA_DTYPE_BF16 = 0
 MLA_DTYPE_F16 = 1
 MLA_SCHED_WORDS = 8
 MLA_DEFAULT_SPLIT_OVERHEAD = 3  # pages; the default schedule's per-split overhead
+MLA_KV_NATIVE = 0
+MLA_KV_FP8_E4M3 = 1
 MLA_DIM_QK = 576
 MLA_DIM_V = 512
 MLA_PAGE_TOKENS = 64
@@ -83,6 +85,11 @@ class MlaDecodeArgs(ctypes.Structure):
         ("lse", _vp),
         ("workspace", _vp),
         ("workspace_bytes", _i64),
+        ("kv_format", _i32),
+        ("kv_reserved", _i32),
+        ("kv_scale", _vp),
+        ("kv_scale_stride_page", _i64),
+        ("kv_scale_stride_blk", _i64),
     ]
 
 
@@ -108,6 +115,11 @@ class MlaKvAppendArgs(ctypes.Structure):
         ("max_pages", _i32),
         ("cache_seqlens", _vp),
         ("status", _vp),
+        ("kv_format", _i32),
+        ("kv_reserved", _i32),
+        ("kv_scale", _vp),
+        ("kv_scale_stride_page", _i64),
+        ("kv_scale_stride_blk", _i64),
     ]
 
 

@@ -9,6 +9,9 @@
   the call at handmade/bench_metax_flashmla.py:33-35.
 * ``mla_decode_with_kvcache(q, kv_cache, block_table, cache_seqlens, num_splits=None,
   sm_scale=None, causal=True)`` -> ``(out, lse)``: one call that schedules and decodes.
+* ``Fp8KVCache`` / ``fp8_kv_cache(num_blocks)`` / ``quantize_kv_cache(kv_cache)``: the fp8
+  latent cache (OCP e4m3 codes with power-of-two scales per token and 128 dims, bf16 rope),
+  accepted wherever a kv cache is, and written by ``kv_append``.
 
 Tensors live on the GPU; every call goes through the C ABI of ``include/mla_decode_amd.h``
 on torch's current stream.  Shapes: q ``[B, s_q, H, 576]``, kv cache ``[num_blocks, 64, 1,
@@ -21,13 +24,13 @@ from __future__ import annotations
 import ctypes
 import math
 import threading
-from typing import Optional, Sequence, Tuple, Union
+from typing import NamedTuple, Optional, Sequence, Tuple, Union
 
 import torch
 
 from . import _lib
-from ._lib import (MLA_DIM_QK, MLA_DIM_V, MLA_DTYPE_BF16, MLA_DTYPE_F16, MlaDecodeArgs,
-                   MlaKvAppendArgs, check)
+from ._lib import (MLA_DIM_QK, MLA_DIM_V, MLA_DTYPE_BF16, MLA_DTYPE_F16, MLA_KV_FP8_E4M3,
+                   MLA_KV_NATIVE, MlaDecodeArgs, MlaKvAppendArgs, check)
 
 _DTYPES = {torch.bfloat16: MLA_DTYPE_BF16, torch.float16: MLA_DTYPE_F16}
 
@@ -125,7 +128,43 @@ def get_mla_metadata_host(cache_seqlens: Sequence[int], num_parts: int, fixed_ov
     return sched, splits
 
 
+class Fp8KVCache(NamedTuple):
+    """The fp8 latent cache: ``latent`` uint8 ``[num_blocks, 64, 512]`` OCP e4m3 codes,
+    ``scale`` fp32 ``[num_blocks, 4, 64]`` (power-of-two scale of 128-dim block j of token
+    row r at ``[page, j, r]``), ``rope`` bf16 ``[num_blocks, 64, 64]``.  Latent value d of a
+    token is ``e4m3(code_d) * scale[d // 128]``.  No counterpart in the reference (its
+    design notes list an fp8 KV cache as unexplored, docs/mla_decode_best_implementation.md:1693).
+    """
+    latent: torch.Tensor
+    scale: torch.Tensor
+    rope: torch.Tensor
+
+
+def fp8_kv_cache(num_blocks: int, device="cuda") -> Fp8KVCache:
+    """An empty (zero) fp8 cache of ``num_blocks`` pages; fill it with ``kv_append``."""
+    return Fp8KVCache(torch.zeros(num_blocks, _lib.MLA_PAGE_TOKENS, MLA_DIM_V, dtype=torch.uint8, device=device),
+                      torch.ones(num_blocks, 4, _lib.MLA_PAGE_TOKENS, dtype=torch.float32, device=device),
+                      torch.zeros(num_blocks, _lib.MLA_PAGE_TOKENS, MLA_DIM_QK - MLA_DIM_V,
+                                  dtype=torch.bfloat16, device=device))
+
+
+def quantize_kv_cache(kv_cache: torch.Tensor) -> Fp8KVCache:
+    """Quantize every page of a bf16 cache ``[num_blocks, 64, 1, 576]`` to the fp8 format
+    (on the GPU, through ``mla_kv_append``: page i is appended as one 64-token sequence)."""
+    _require_gpu(kv_cache, "kv_cache")
+    if kv_cache.dtype != torch.bfloat16 or kv_cache.shape[-1] != MLA_DIM_QK or kv_cache.shape[1] != _lib.MLA_PAGE_TOKENS:
+        raise ValueError("kv_cache must be a bf16 [num_blocks, 64, 1, 576] tensor")
+    nb = kv_cache.shape[0]
+    dst = fp8_kv_cache(nb, kv_cache.device)
+    table = torch.arange(nb, dtype=torch.int32, device=kv_cache.device).reshape(nb, 1)
+    lens = torch.zeros(nb, dtype=torch.int32, device=kv_cache.device)
+    kv_append(kv_cache.reshape(nb, _lib.MLA_PAGE_TOKENS, MLA_DIM_QK), dst, table, lens)
+    return dst
+
+
 def _split_kv(kv_cache) -> Tuple[torch.Tensor, torch.Tensor]:
+    if isinstance(kv_cache, Fp8KVCache):
+        raise ValueError("an fp8 cache has no bf16 latent half")
     if isinstance(kv_cache, (tuple, list)):
         latent, rope = kv_cache
         if latent.shape[-1] != MLA_DIM_V or rope.shape[-1] != MLA_DIM_QK - MLA_DIM_V:
@@ -150,13 +189,20 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
         raise ValueError(f"q must be [B, s_q, H, {MLA_DIM_QK}]")
     if q.dtype not in _DTYPES:
         raise ValueError("q must be bfloat16 or float16")
-    latent, rope = _split_kv(kv_cache)
-    for t, n in ((latent, "kv latent"), (rope, "kv rope")):
-        _require_gpu(t, n)
-        if t.dtype != q.dtype:
-            raise ValueError("kv cache dtype must match q")
-        if t.dim() != 4 or t.shape[1] != _lib.MLA_PAGE_TOKENS or t.shape[2] != 1 or t.stride(-1) != 1:
-            raise ValueError("kv cache must be [num_blocks, 64, 1, D] with unit stride in D")
+    fp8 = isinstance(kv_cache, Fp8KVCache)
+    if fp8:
+        latent, scale, rope = _check_fp8_cache(kv_cache)
+        if q.dtype != torch.bfloat16:
+            raise ValueError("the fp8 cache is read with bf16 queries")
+    else:
+        latent, rope = _split_kv(kv_cache)
+        scale = None
+        for t, n in ((latent, "kv latent"), (rope, "kv rope")):
+            _require_gpu(t, n)
+            if t.dtype != q.dtype:
+                raise ValueError("kv cache dtype must match q")
+            if t.dim() != 4 or t.shape[1] != _lib.MLA_PAGE_TOKENS or t.shape[2] != 1 or t.stride(-1) != 1:
+                raise ValueError("kv cache must be [num_blocks, 64, 1, D] with unit stride in D")
     if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
         raise ValueError("block_table must be a [B, P] int32 tensor with unit column stride")
     if cache_seqlens.dtype != torch.int32 or cache_seqlens.dim() != 1:
@@ -195,6 +241,10 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
     a.kv_nope, a.kv_rope = latent.data_ptr(), rope.data_ptr()
     a.kv_stride_page, a.kv_stride_tok, a.kv_stride_batch = latent.stride(0), latent.stride(1), 0
     a.kv_rope_stride_page, a.kv_rope_stride_tok, a.kv_rope_stride_batch = rope.stride(0), rope.stride(1), 0
+    a.kv_format = MLA_KV_FP8_E4M3 if fp8 else MLA_KV_NATIVE
+    if fp8:
+        a.kv_scale = scale.data_ptr()
+        a.kv_scale_stride_page, a.kv_scale_stride_blk = scale.stride(0), scale.stride(1)
     a.block_table = block_table.data_ptr()
     a.block_table_stride = block_table.stride(0)
     a.num_parts = num_parts
@@ -206,7 +256,7 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
     a.lse = lse.data_ptr()
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws_bytes
-    keep = (q, latent, rope, block_table, seqlens, sched, splits, out, lse, ws)
+    keep = (q, latent, rope, scale, block_table, seqlens, sched, splits, out, lse, ws)
     return a, out, lse, keep
 
 
@@ -296,17 +346,24 @@ def kv_append(kv_new: torch.Tensor, kv_cache, block_table: torch.Tensor,
     Returns the filled C argument struct (for re-launching through the C ABI directly).
     """
     _require_gpu(kv_new, "kv_new")
-    latent, rope = _split_kv(kv_cache)
+    fp8 = isinstance(kv_cache, Fp8KVCache)
+    if fp8:
+        latent, scale, rope = _check_fp8_cache(kv_cache)
+    else:
+        latent, rope = _split_kv(kv_cache)
     if kv_new.dim() == 4:
         if kv_new.shape[2] != 1:
             raise ValueError("kv_new [B, n_new, 1, 576] must have one KV head")
         kv_new = kv_new[:, :, 0]
     if kv_new.dim() != 3 or kv_new.shape[-1] != MLA_DIM_QK:
         raise ValueError("kv_new must be [B, n_new, 576]")
-    if kv_new.dtype not in _DTYPES or latent.dtype != kv_new.dtype or rope.dtype != kv_new.dtype:
+    if fp8:
+        if kv_new.dtype != torch.bfloat16:
+            raise ValueError("the fp8 cache takes bf16 tokens")
+    elif kv_new.dtype not in _DTYPES or latent.dtype != kv_new.dtype or rope.dtype != kv_new.dtype:
         raise ValueError("kv_new and the cache must share one 16-bit dtype (bf16 or fp16)")
     B, n_new = kv_new.shape[0], kv_new.shape[1]
-    if latent.dim() != 4 or latent.shape[1] != _lib.MLA_PAGE_TOKENS or latent.shape[2] != 1:
+    if not fp8 and (latent.dim() != 4 or latent.shape[1] != _lib.MLA_PAGE_TOKENS or latent.shape[2] != 1):
         raise ValueError("kv_cache must be [num_blocks, 64, 1, 576] (or a latent / rope pair)")
     if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B:
         raise ValueError("block_table must be [B, max_pages] int32")
@@ -329,8 +386,27 @@ def kv_append(kv_new: torch.Tensor, kv_cache, block_table: torch.Tensor,
     a.block_table_stride, a.max_pages = block_table.stride(0), block_table.shape[1]
     a.cache_seqlens = cache_seqlens.data_ptr()
     a.status = status.data_ptr() if status is not None else None
+    if fp8:
+        a.kv_format = MLA_KV_FP8_E4M3
+        a.kv_scale = scale.data_ptr()
+        a.kv_scale_stride_page, a.kv_scale_stride_blk = scale.stride(0), scale.stride(1)
     check("mla_kv_append", _lib.load().mla_kv_append(ctypes.byref(a), _stream_ptr(kv_new.device)))
     return a
+
+
+def _check_fp8_cache(c: Fp8KVCache):
+    latent, scale, rope = c.latent, c.scale, c.rope
+    for t, n in ((latent, "fp8 latent"), (scale, "fp8 scale"), (rope, "fp8 rope")):
+        _require_gpu(t, n)
+    nb, page = latent.shape[0], _lib.MLA_PAGE_TOKENS
+    if latent.dtype not in (torch.uint8, torch.float8_e4m3fn) or latent.dim() != 3 or \
+            latent.shape[1:] != (page, MLA_DIM_V) or latent.stride(-1) != 1:
+        raise ValueError("fp8 latent must be a uint8 / float8_e4m3fn [num_blocks, 64, 512] tensor")
+    if scale.dtype != torch.float32 or scale.shape != (nb, 4, page) or scale.stride(-1) != 1:
+        raise ValueError("fp8 scale must be a float32 [num_blocks, 4, 64] tensor")
+    if rope.dtype != torch.bfloat16 or rope.shape != (nb, page, MLA_DIM_QK - MLA_DIM_V) or rope.stride(-1) != 1:
+        raise ValueError("fp8 rope must be a bf16 [num_blocks, 64, 64] tensor")
+    return latent, scale, rope
 
 
 def default_sm_scale() -> float:

@@ -82,6 +82,10 @@ struct KParams {
   float* lse;
   float* ws_lse;    // [slots, rows] log2-domain lse of each split
   uint16_t* ws_o;   // [slots, rows, 512] softmax-normalised partial outputs, input dtype
+  // fp8 latent cache only: kv_nope holds e4m3 codes (strides in bytes) and kv_scale the fp32
+  // power-of-two scales, [page][128-dim block][token] with strides ks_sp, ks_sb (floats)
+  const float* kv_scale;
+  int64_t ks_sp, ks_sb;
   int32_t batch, s_q, heads, rows, causal, num_parts;
   float scale_log2;  // sm_scale * log2(e)
 };
@@ -264,11 +268,11 @@ __device__ __forceinline__ void issue_stage(uint8_t LDS_AS* slot, const uint16_t
   }
 }
 
-template <int NW, int NSTAGE>
+template <int PER, int NSTAGE>
 __device__ __forceinline__ void wait_stage(int after) {
-  // Wait until this wave's loads of the oldest outstanding stage have landed, with
-  // `after` younger stages allowed to stay in flight.
-  constexpr int per = kLoadsPerStage / NW;
+  // Wait until this wave's loads of the oldest outstanding stage have landed (PER loads per
+  // stage and wave), with `after` younger stages allowed to stay in flight.
+  constexpr int per = PER;
   if constexpr (NSTAGE >= 4) {
     if (after >= 2) { wait_vmcnt<(2 * per < 64 ? 2 * per : 0)>(); return; }
   }
@@ -286,6 +290,62 @@ __device__ __forceinline__ i32x4 lds_tr_pair(const uint8_t LDS_AS* p) {
   const i32x2 lo2 = __builtin_bit_cast(i32x2, lo);
   const i32x2 hi2 = __builtin_bit_cast(i32x2, hi);
   return i32x4{lo2.x, lo2.y, hi2.x, hi2.y};
+}
+
+// ---------------------------------------------------------------------------------------
+// fp8 latent cache: stage layout, loads and fragment conversion
+// ---------------------------------------------------------------------------------------
+// A stage of the fp8 cache (32 token rows, 24 KiB of LDS):
+//   - latent codes: block q*4 + s (q = row group 0..3: rows 8q .. 8q+7; s = 128-byte segment
+//     0..3 of the 512-byte row) holds 16-byte chunk c16 of row r at slot
+//     8*(r%8) + (c16 ^ swz8(r)),  swz8(r) = (r%8)/2 + 4*((r/8 ^ r/16) & 1);
+//   - rope (bf16): 16 KiB + block q, 16-byte chunk c (8 dims) of row r at slot
+//     8*(r%8) + (c ^ swzr(r)),  swzr(r) = (r%8)/2 + 4*((r/8) & 1);
+//   - scales: 20 KiB + 1 KiB * blk, the fp32 scale of 128-dim block blk of token t at byte 4t.
+// Every latent and rope load reads eight whole 128-byte lines.  The swizzles keep the QK
+// fragment reads (8 bytes of 16 rows x 2 lane groups, or 16 bytes of 16 rows) and the
+// transposed V^T reads (8 rows x 16 bytes per lane-group pair) free of bank conflicts.
+constexpr int kStageBytes8 = 24 * 1024;
+constexpr int kLoadsPerStage8 = 24;
+constexpr int kRopeOff8 = 16 * 1024;
+constexpr int kScaleOff8 = 20 * 1024;
+__device__ __forceinline__ int swz8(int r) { return ((r & 7) >> 1) | ((((r >> 3) ^ (r >> 4)) & 1) << 2); }
+__device__ __forceinline__ int swzr(int r) { return ((r & 7) >> 1) | (((r >> 3) & 1) << 2); }
+
+template <int NL>
+__device__ __forceinline__ void issue_stage8(uint8_t LDS_AS* slot, const uint8_t* lat_base,
+                                             const uint16_t* rope_base, const float* scale_base,
+                                             int lat_st, int rope_st, int64_t scale_sb,
+                                             int last_row, int wave, int lane) {
+  // NL = 4: wave w loads row group w's 4 latent blocks and rope block, and the scales of
+  // 128-dim block w; NL = 1: the wave loads all 24 blocks.
+  static_assert(NL == 1 || NL == 4, "stage loads are split over one or four waves");
+#pragma unroll
+  for (int qi = 0; qi < 4 / NL; ++qi) {
+    const int q = NL == 1 ? qi : wave;  // uniform
+    const int r = 8 * q + (lane >> 3);  // LDS row; rows past the sequence end re-read its last row
+    const int row = r < last_row ? r : last_row;
+    const uint32_t on = (uint32_t)(row * lat_st) + (uint32_t)(((lane & 7) ^ swz8(r)) << 4);
+    const uint32_t orp = (uint32_t)(row * rope_st) * 2 + (uint32_t)(((lane & 7) ^ swzr(r)) << 4);
+#pragma unroll
+    for (int sg = 0; sg < 4; ++sg)
+      dma16(lat_base + 128 * sg, on, (uint32_t)(uintptr_t)(slot + (q * 4 + sg) * 1024));
+    dma16(rope_base, orp, (uint32_t)(uintptr_t)(slot + kRopeOff8 + q * 1024));
+    // 32 token scales of block q: lanes 0..7 fetch 16 bytes each, the others repeat them
+    dma16(scale_base + q * scale_sb, (uint32_t)((lane & 7) << 4),
+          (uint32_t)(uintptr_t)(slot + kScaleOff8 + q * 1024));
+  }
+}
+
+// Two OCP e4m3 codes (bytes 2*hi, 2*hi+1 of w) to two bf16 values times 2^exponent(scale).
+template <bool HI>
+__device__ __forceinline__ int cvt_fp8x2(int w, float scale) {
+  return __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, scale, HI));
+}
+__device__ __forceinline__ i32x4 cvt_fp8x8(i32x2 raw, float scale) {
+  const int x = raw.x, y = raw.y;  // elements copied out before use (see the bit_cast note)
+  return i32x4{cvt_fp8x2<false>(x, scale), cvt_fp8x2<true>(x, scale), cvt_fp8x2<false>(y, scale),
+               cvt_fp8x2<true>(y, scale)};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -325,22 +385,31 @@ constexpr int waves_per_simd(int nw, int ht, int nstage, bool ws) {
 //    stages into its own one-stage slot with no barrier between waves; their accumulators are
 //    merged through LDS at the end of the segment, so the workgroup leaves one partial where
 //    NW single-wave workgroups would leave NW.
-template <int DT, int NW, int HT, int NSTAGE, bool WS>
+// KV8: the latent cache holds OCP e4m3 codes with power-of-two scales per token and 128-dim
+// block (bf16 queries and rope); K fragments are converted to bf16 with their scale on the way
+// from LDS to the MFMA, V^T fragments without it, and the scales of V are folded into P^T.
+template <int DT, int NW, int HT, int NSTAGE, bool WS, bool KV8>
 __global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW > 0
                                           ? waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW : 1)
 void mla_splitkv_kernel(KParams p) {
   static_assert(NW == 1 || NW == 4, "one or four waves per workgroup");
   static_assert(!WS || NSTAGE == 1, "wave-split workgroups give each wave a one-stage slot");
+  static_assert(!KV8 || DT == MLA_DTYPE_BF16, "the fp8 cache is read with bf16 queries");
+  constexpr int kSB = KV8 ? kStageBytes8 : kStageBytes;      // bytes of one stage in LDS
+  constexpr int kLPS = KV8 ? kLoadsPerStage8 : kLoadsPerStage;  // wave-wide loads per stage
   constexpr int NL = WS ? 1 : NW;  // waves sharing the loads of one stage
   constexpr int LEAD = NSTAGE - 1;
-  static_assert((NSTAGE - 1) * (kLoadsPerStage / NL) < 64, "outstanding stage loads exceed vmcnt");
-  static_assert(kLoadsPerStage % NL == 0, "loads per stage must split evenly");
+  static_assert((NSTAGE - 1) * (kLPS / NL) < 64, "outstanding stage loads exceed vmcnt");
+  static_assert(kLPS % NL == 0, "loads per stage must split evenly");
   constexpr int R = WS ? 16 * HT : NW * 16 * HT;
   constexpr int DK = 4;  // LDS prefetch depth of the QK A fragments
   constexpr int DV = HT == 2 ? 2 : 4;  // LDS prefetch depth of the PV A fragments
   constexpr float kTau = ref_tau<DT>();
   constexpr int kSlots = WS ? NW : NSTAGE;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSlots * kStageBytes];
+  constexpr int kMergePitch = kDV * 4 + 16;  // wave-split merge: fp32 rows of 512, padded
+  constexpr int kMergeBytes = WS ? NW * 16 * kMergePitch : 0;
+  constexpr int kSmem = kSlots * kSB > kMergeBytes ? kSlots * kSB : kMergeBytes;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSmem];
   // wave-split merge words: (row max, row sum) per wave and row
   __shared__ float merge_sh[WS ? NW : 1][2][16];
   // "score above reference" words, one per stage modulo 4.  A wave whose stage-k scores exceed
@@ -360,7 +429,7 @@ void mla_splitkv_kernel(KParams p) {
   const int li = lane & 15;  // lane within group
   const int row0 = hb * R + (WS ? 0 : wave * 16 * HT);
   // this wave's stage ring, and the first stage / stride of its turn over a segment
-  uint8_t LDS_AS* const ring = smem + (WS ? wave * kStageBytes : 0);
+  uint8_t LDS_AS* const ring = smem + (WS ? wave * kSB : 0);
   const int k0 = WS ? wave : 0;
   constexpr int kStep = WS ? NW : 1;
 
@@ -385,6 +454,19 @@ void mla_splitkv_kernel(KParams p) {
   const int rv = 4 * g + (li >> 2);
   const int v_lane = (rv >> 3) * 9216 + ((rv & 7) << 7) + (((li >> 1) & 1) ^ stage_swz(rv)) * 16 +
                      ((li & 1) << 3);
+  // fp8 layout (KV8).  QK: latent fragment (kk < 16, tt) = token row 16tt + li, dims
+  // 32kk + 8g .. +7 (8 bytes): block (2tt + li/8)*4 + kk/4, chunk 2(kk%4) + g/2, half g%2; with
+  // swz8(16tt + li) = swz8(li) ^ 4tt the address is (kb8 ^ 32(kk%4) ^ 64tt) + 8192tt +
+  // 1024(kk/4).  Rope fragment kk = 16 + j: chunk 4j + g of rope block 2tt + li/8, address
+  // (kr8 ^ 64j) + 2048tt.  PV: lane li of group g addresses token t8 = (li/2 < 4 ? 4g + li/2 :
+  // 12 + 4g + li/2), byte half li%2 of chunk dt%8 in block (t8/8)*4 + dt/8; ds_read_b64_tr_b8
+  // hands lane li the 8 tokens its group addressed at dim 16dt + li, i.e. the V^T A operand
+  // whose k order (tokens 4g..4g+3, 16+4g..16+4g+3) is that of P^T.  Address of tile dt:
+  // (v8_lane ^ 16(dt%8)) + 1024(dt/8).
+  const int kb8 = (li >> 3) * 4096 + ((((li & 7) << 3) + ((g >> 1) ^ swz8(li))) << 4) + ((g & 1) << 3);
+  const int kr8 = kRopeOff8 + (li >> 3) * 1024 + ((((li & 7) << 3) + (g ^ swzr(li))) << 4);
+  const int t8 = (li >> 1) < 4 ? 4 * g + (li >> 1) : 12 + 4 * g + (li >> 1);
+  const int v8_lane = (t8 >> 3) * 4096 + ((((t8 & 7) << 3) + swz8(t8)) << 4) + ((li & 1) << 3);
 
   const int kv_st = (int)p.kv_st, kr_st = (int)p.kr_st;
   const bool paged = p.block_table != nullptr;
@@ -415,9 +497,15 @@ void mla_splitkv_kernel(KParams p) {
       const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 16 * g;
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
-        // dims 8*sigma(kk, g) = 64*(kk/2) + 16*g + 8*(kk%2)
-        const int d = 64 * (kk >> 1) + 8 * (kk & 1);
-        qf[ht][kk] = *(const i32x4*)(d < kRopeOff ? qn + d : qr + (d - kRopeOff));
+        if constexpr (KV8) {
+          // dims 32kk + 8g (the fp8 fragments' natural order)
+          const int d = 32 * kk - 8 * g;  // qn / qr already point 16g past the row start
+          qf[ht][kk] = *(const i32x4*)(kk < 16 ? qn + d : qr + (d - kRopeOff));
+        } else {
+          // dims 8*sigma(kk, g) = 64*(kk/2) + 16*g + 8*(kk%2)
+          const int d = 64 * (kk >> 1) + 8 * (kk & 1);
+          qf[ht][kk] = *(const i32x4*)(d < kRopeOff ? qn + d : qr + (d - kRopeOff));
+        }
       }
     }
     const int lmin = L - (p.causal ? p.s_q - 1 : 0);  // every row sees tokens < lmin
@@ -440,6 +528,19 @@ void mla_splitkv_kernel(KParams p) {
 
     auto issue = [&](int k) __attribute__((always_inline)) {
       const int st = st_begin + k;
+      if constexpr (KV8) {  // paged only (checked by the host)
+        const int pidx = st >> 1;
+        if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
+        const int pg = __builtin_amdgcn_readlane(bt_lane, pidx - pbase);
+        const int tok = (st & 1) * kStageTok;
+        const uint8_t* lb = (const uint8_t*)p.kv_nope + ((int64_t)pg * p.kv_sp + tok * kv_st);
+        const uint16_t* rb = p.kv_rope + ((int64_t)pg * p.kr_sp + tok * kr_st);
+        const float* scb = p.kv_scale + ((int64_t)pg * p.ks_sp + tok);
+        const int left = L - st * kStageTok;
+        issue_stage8<NL>(ring + (k % NSTAGE) * kSB, lb, rb, scb, kv_st, kr_st, p.ks_sb,
+                         (left < kStageTok ? left : kStageTok) - 1, NL == 1 ? 0 : wave, lane);
+        return;
+      }
       const uint16_t* nb;
       const uint16_t* rb;
       if (paged) {
@@ -454,7 +555,7 @@ void mla_splitkv_kernel(KParams p) {
         rb = p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st);
       }
       const int left = L - st * kStageTok;
-      issue_stage<NL>(ring + (k % NSTAGE) * kStageBytes, nb, rb, kv_st, kr_st,
+      issue_stage<NL>(ring + (k % NSTAGE) * kSB, nb, rb, kv_st, kr_st,
                       (left < kStageTok ? left : kStageTok) - 1, NL == 1 ? 0 : wave, lane);
     };
 
@@ -500,7 +601,7 @@ void mla_splitkv_kernel(KParams p) {
 
       // ---- O^T += V^T P^T over the 32 tokens of stage kp; DV fragments in flight
       auto v_base = [&](int kp) __attribute__((always_inline)) {
-        const uint8_t LDS_AS* vb = ring + (kp % NSTAGE) * kStageBytes + v_lane;
+        const uint8_t LDS_AS* vb = ring + (kp % NSTAGE) * kSB + v_lane;
         asm volatile("" : "+v"(vb));
         return vb;
       };
@@ -535,13 +636,95 @@ void mla_splitkv_kernel(KParams p) {
         // write to their registers can be placed before it.
         operand_guard<HT>(pb, vf[(kDimTiles - 1) % DV]);
       };
+      // fp8 cache: V^T fragment t (natural dim-tile order) as raw codes, converted at use
+      auto v8_base = [&](int kp) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* vb = ring + (kp % NSTAGE) * kSB + v8_lane;
+        asm volatile("" : "+v"(vb));
+        return vb;
+      };
+      auto v8_raw = [&](const uint8_t LDS_AS* vb, int t) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* xb =
+            (t & 7) ? (const uint8_t LDS_AS*)(uintptr_t)((uint32_t)(uintptr_t)vb ^ (uint32_t)(16 * (t & 7))) : vb;
+        return __builtin_amdgcn_ds_read_tr8_b64_v2i32((i32x2 LDS_AS*)(xb + 1024 * (t >> 3)));
+      };
+      auto v8_prefetch = [&](int kp, i32x2 (&vr)[DV]) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* vb = v8_base(kp);
+#pragma unroll
+        for (int n = 0; n < DV; ++n) vr[n] = v8_raw(vb, n);
+      };
+      // O^T += V^T (P^T * s): the scales of V (per token and 128-dim block) multiply P^T, once
+      // per block of eight dim tiles.  On the sequence's last stage the scales of rows past its
+      // end are not data (their P is 0): they are replaced by 0 so that 0 * s stays 0.
+      auto pv_stage8 = [&](int kp, const float (&pvf)[HT][8], i32x2 (&vr)[DV]) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* vb = v8_base(kp);
+        const uint8_t LDS_AS* scb = ring + (kp % NSTAGE) * kSB + kScaleOff8 + 16 * g;
+        const int left = L - (st_begin + kp) * kStageTok;
+        // P^T * s for 128-dim block bk
+        auto make_pb = [&](int bk, i32x4 (&pbo)[HT]) __attribute__((always_inline)) {
+          f32x4 s0 = *(const f32x4 LDS_AS*)(scb + bk * 1024);       // tokens 4g .. 4g+3
+          f32x4 s1 = *(const f32x4 LDS_AS*)(scb + bk * 1024 + 64);  // tokens 16+4g ..
+          if (left < kStageTok) {  // uniform
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              s0[i] = 4 * g + i < left ? s0[i] : 0.f;
+              s1[i] = 16 + 4 * g + i < left ? s1[i] : 0.f;
+            }
+          }
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht)
+            pbo[ht] = i32x4{(int)pack2<DT>(pvf[ht][0] * s0[0], pvf[ht][1] * s0[1]),
+                            (int)pack2<DT>(pvf[ht][2] * s0[2], pvf[ht][3] * s0[3]),
+                            (int)pack2<DT>(pvf[ht][4] * s1[0], pvf[ht][5] * s1[1]),
+                            (int)pack2<DT>(pvf[ht][6] * s1[2], pvf[ht][7] * s1[3])};
+        };
+        // As in the QK loop: the operands of tile t+1 (V^T conversion, and P^T * s at a block
+        // start) are produced before MFMA t issues, and the operands of tile t-1 stay live until
+        // MFMA t has issued.
+        i32x4 pbb[HT], pbb_old[HT];
+        make_pb(0, pbb);
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) pbb_old[ht] = pbb[ht];
+        i32x4 a_cur = cvt_fp8x8(vr[0], 1.0f);
+        vr[0] = v8_raw(vb, DV);
+        i32x4 a_prev = a_cur;
+#pragma unroll
+        for (int t = 0; t < kDimTiles; ++t) {
+          i32x4 a_next = a_cur;
+          i32x4 pbb_next[HT];
+          const bool new_block = t + 1 < kDimTiles && ((t + 1) & 7) == 0;
+          if (t + 1 < kDimTiles) {
+            a_next = cvt_fp8x8(vr[(t + 1) % DV], 1.0f);
+            if (t + 1 + DV < kDimTiles) vr[(t + 1) % DV] = v8_raw(vb, t + 1 + DV);
+          }
+          if (new_block) make_pb((t + 1) >> 3, pbb_next);
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) o[t][ht] = mfma32<DT>(a_cur, pbb[ht], o[t][ht]);
+          asm volatile("" ::"v"(a_prev));
+          if ((t & 7) == 0 && t > 0) {
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) asm volatile("" ::"v"(pbb_old[ht]));
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          a_prev = a_cur;
+          a_cur = a_next;
+          if (new_block) {
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) {
+              pbb_old[ht] = pbb[ht];
+              pbb[ht] = pbb_next[ht];
+            }
+          }
+        }
+        operand_guard<HT>(pbb, a_prev);
+      };
+
       bool abort = false;
       // wave-split: this wave's own "score above reference" flag of its previous stage
       bool over_prev = false;
 #pragma unroll 1
       for (int j = 0, k = k0; k < nst; ++j, k += kStep) {  // j: the wave's own stage count
         const int remaining_after = nst - 1 - k;
-        wait_stage<NL, NSTAGE>(remaining_after < LEAD - 1 ? remaining_after : LEAD - 1);
+        wait_stage<kLPS / NL, NSTAGE>(remaining_after < LEAD - 1 ? remaining_after : LEAD - 1);
         if constexpr (!WS) lds_barrier();
         // the previous stage's flags, read now and tested after this stage's QK product
         int prev_over = 0;
@@ -557,7 +740,7 @@ void mla_splitkv_kernel(KParams p) {
           if (k + LEAD < nst) issue(k + LEAD);
         }
 
-        const uint8_t LDS_AS* sb = ring + (k % NSTAGE) * kStageBytes;
+        const uint8_t LDS_AS* sb = ring + (k % NSTAGE) * kSB;
         const int st = st_begin + k;
 
         // ---- S^T = K Q^T over 576 dims: two 16-token tiles x HT 16-row tiles.
@@ -572,20 +755,86 @@ void mla_splitkv_kernel(KParams p) {
         asm volatile("" : "+v"(kb1));
 #define MLA_KFRAG(N) \
   (*(const i32x4 LDS_AS*)((((N) >> 1) & 1 ? kb1 : kb0) + ((N) & 1) * kPanelBytes + ((N) >> 2) * 1024))
+        // fp8: the K scales of rows li and 16 + li, per 128-dim block
+        float sk[2][4];
+        const uint8_t LDS_AS* kbl = sb + kb8;
+        const uint8_t LDS_AS* kbr = sb + kr8;
+        if constexpr (KV8) {
 #pragma unroll
-        for (int n = 0; n < DK; ++n) kf[n] = MLA_KFRAG(n);
+          for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int n = 0; n < 2 * kKSteps; ++n) {
-          const i32x4 a = kf[n % DK];
-          if (n + DK < 2 * kKSteps) kf[n % DK] = MLA_KFRAG(n + DK);
-#pragma unroll
-          for (int ht = 0; ht < HT; ++ht) {
-            if (n < 2)
-              mfma_qk_first<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
-            else
-              mfma_qk<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
+            for (int bk = 0; bk < 4; ++bk)
+              sk[tt][bk] = *(const float LDS_AS*)(sb + kScaleOff8 + bk * 1024 + 4 * (16 * tt + li));
+          asm volatile("" : "+v"(kbl));
+          asm volatile("" : "+v"(kbr));
+        }
+        // fp8 fragment n = 2*kk + tt as raw data: 8 codes (latent) or 8 bf16 values (rope)
+        auto k8_raw = [&](int n) __attribute__((always_inline)) -> i32x4 {
+          const int kk = n >> 1, tt = n & 1;
+          if (kk < 16) {
+            const uint32_t x = (uint32_t)((32 * (kk & 3)) ^ (64 * tt));  // bits 5-6 only
+            const uint8_t LDS_AS* a = x ? (const uint8_t LDS_AS*)(uintptr_t)((uint32_t)(uintptr_t)kbl ^ x) : kbl;
+            const i32x2 r = *(const i32x2 LDS_AS*)(a + 8192 * tt + 1024 * (kk >> 2));
+            const int r0 = r.x, r1 = r.y;
+            return i32x4{r0, r1, 0, 0};
           }
-          __builtin_amdgcn_sched_barrier(0);
+          const uint8_t LDS_AS* a =
+              kk == 16 ? kbr : (const uint8_t LDS_AS*)(uintptr_t)((uint32_t)(uintptr_t)kbr ^ 64u);
+          return *(const i32x4 LDS_AS*)(a + 2048 * tt);
+        };
+        if constexpr (KV8) {
+          // The converted fragments are VALU results read by the (inline-asm) MFMAs, whose
+          // hazards the compiler does not see.  Fragment n+1 is converted before MFMA n issues
+          // (so an MFMA separates every conversion from its reader), and fragment n-1 is held
+          // live until MFMA n has issued (so no conversion overwrites the operands of the MFMA
+          // just issued).
+          auto k8_conv = [&](int n, const i32x4& raw) __attribute__((always_inline)) -> i32x4 {
+            if ((n >> 1) < 16) {
+              const int r0 = raw.x, r1 = raw.y;
+              return cvt_fp8x8(i32x2{r0, r1}, sk[n & 1][n >> 3]);
+            }
+            return raw;
+          };
+#pragma unroll
+          for (int n = 0; n < DK; ++n) kf[n] = k8_raw(n);
+          i32x4 c_cur = k8_conv(0, kf[0]);
+          kf[0] = k8_raw(DK);
+          i32x4 c_prev = c_cur;
+#pragma unroll
+          for (int n = 0; n < 2 * kKSteps; ++n) {
+            i32x4 c_next = c_cur;
+            if (n + 1 < 2 * kKSteps) {
+              c_next = k8_conv(n + 1, kf[(n + 1) % DK]);
+              if (n + 1 + DK < 2 * kKSteps) kf[(n + 1) % DK] = k8_raw(n + 1 + DK);
+            }
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) {
+              if (n < 2)
+                mfma_qk_first<DT>(acc[ht][n & 1], c_cur, qf[ht][n >> 1]);
+              else
+                mfma_qk<DT>(acc[ht][n & 1], c_cur, qf[ht][n >> 1]);
+            }
+            asm volatile("" ::"v"(c_prev));
+            __builtin_amdgcn_sched_barrier(0);
+            c_prev = c_cur;
+            c_cur = c_next;
+          }
+        } else {
+#pragma unroll
+          for (int n = 0; n < DK; ++n) kf[n] = MLA_KFRAG(n);
+#pragma unroll
+          for (int n = 0; n < 2 * kKSteps; ++n) {
+            const i32x4 a = kf[n % DK];
+            if (n + DK < 2 * kKSteps) kf[n % DK] = MLA_KFRAG(n + DK);
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) {
+              if (n < 2)
+                mfma_qk_first<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
+              else
+                mfma_qk<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
 #undef MLA_KFRAG
         qk_settle(acc[0][0]);
@@ -601,8 +850,10 @@ void mla_splitkv_kernel(KParams p) {
           }
         }
         i32x4 vf[DV];
+        i32x2 vr[DV];
         if constexpr (MODE != kPassRowMax) {
-          v_prefetch(k, vf);
+          if constexpr (KV8) v8_prefetch(k, vr);
+          else v_prefetch(k, vf);
         }
 
         // ---- mask tokens past each row's limit (sequence tail / causal)
@@ -655,6 +906,7 @@ void mla_splitkv_kernel(KParams p) {
 
         // ---- P^T = 2^(S^T * sm_scale * log2(e) - m), packed to the B operand of PV
         i32x4 pb[HT];
+        float pvf[HT][8];  // fp8: P kept in fp32 until the per-block scales are applied
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) {
           const float mu = m_ref[ht] == -INFINITY ? 0.f : m_ref[ht];
@@ -665,11 +917,19 @@ void mla_splitkv_kernel(KParams p) {
             for (int r = 0; r < 4; ++r) pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
           l_part[ht] += ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) +
                         ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3]));
-          pb[ht] = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
-                         (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
+          if constexpr (KV8) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) pvf[ht][4 * tt + r] = pv[tt][r];
+          } else {
+            pb[ht] = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
+                           (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
+          }
         }
 
-        pv_stage(k, pb, vf);
+        if constexpr (KV8) pv_stage8(k, pvf, vr);
+        else pv_stage(k, pb, vf);
         refill_single(k);
         if constexpr (MODE == kPassFirstStageRef && !WS) wait_lgkm0();  // flag store lands before the barrier
       }
@@ -714,8 +974,7 @@ void mla_splitkv_kernel(KParams p) {
       // into LDS (fp32 rows of 512 with a 16-byte pad: conflict-free 16-byte stores), then
       // wave w sums and stores dims 128w .. 128w + 127 of all 16 rows.  The slots are free:
       // every wave waited for its own stage loads before the first barrier.
-      constexpr int kMergePitch = kDV * 4 + 16;
-      static_assert(NW * 16 * kMergePitch <= kSlots * kStageBytes, "merge staging exceeds the slots");
+      static_assert(kMergeBytes <= kSmem, "merge staging exceeds the shared memory");
       const int64_t slot = slot0 + split;
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) {
@@ -837,7 +1096,23 @@ struct AppendParams {
   int32_t bt_stride, max_pages, num_blocks, batch, n_new;
   int32_t* seqlens;
   int32_t* status;
+  // fp8 cache (kv8 != 0): kv_nope holds e4m3 codes (strides in bytes), kv_scale the scales
+  int32_t kv8;
+  float* kv_scale;
+  int64_t ks_sp, ks_sb;
 };
+
+// The power-of-two exponent k of a 128-dim block's scale from its bf16 amax (bit pattern
+// `bits`): the smallest k with amax <= 448 * 2^k (448 = 1.75 * 2^8, mantissa 0x60), clamped
+// to [-126, 127]; amax = 0 gives 0.
+__device__ __forceinline__ int fp8_block_exp(uint32_t bits) {
+  const int ef = (int)((bits >> 7) & 0xFF);
+  const int mant = (int)(bits & 0x7F);
+  int k = ef - 127 - 8 + (mant > 0x60 ? 1 : 0);
+  if (ef == 0) k = -126;
+  if (bits == 0) k = 0;
+  return k < -126 ? -126 : (k > 127 ? 127 : k);
+}
 
 __global__ __launch_bounds__(256) void mla_kv_append_kernel(AppendParams a) {
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -865,7 +1140,33 @@ __global__ __launch_bounds__(256) void mla_kv_append_kernel(AppendParams a) {
     const int row = pos & 63;
     const uint16_t* src = a.kv_new + b * a.n_sb + t * a.n_st;
     const i32x4 v = *(const i32x4*)(src + 8 * lane);
-    *(i32x4*)(a.kv_nope + (int64_t)pg * a.kv_sp + (int64_t)row * a.kv_st + 8 * lane) = v;
+    if (a.kv8) {  // uniform
+      // lane l holds dims 8l .. 8l+7; block j (dims 128j ..) is the lane group of 16
+      float x[8];
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int w = v[i];
+        x[2 * i] = __uint_as_float((uint32_t)w << 16);
+        x[2 * i + 1] = __uint_as_float((uint32_t)w & 0xFFFF0000u);
+        amax = fmaxf(amax, fmaxf(fabsf(x[2 * i]), fabsf(x[2 * i + 1])));
+      }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
+      const int k = fp8_block_exp(__float_as_uint(amax) >> 16);  // amax is a bf16 value
+      int lo = 0, hi = 0;
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(x[0], -k), __builtin_ldexpf(x[1], -k), lo, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(x[2], -k), __builtin_ldexpf(x[3], -k), lo, true);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(x[4], -k), __builtin_ldexpf(x[5], -k), hi, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_ldexpf(x[6], -k), __builtin_ldexpf(x[7], -k), hi, true);
+      uint8_t* dst = (uint8_t*)a.kv_nope + (int64_t)pg * a.kv_sp + (int64_t)row * a.kv_st + 8 * lane;
+      *(i32x2*)dst = i32x2{lo, hi};
+      if ((lane & 15) == 0)
+        a.kv_scale[(int64_t)pg * a.ks_sp + (int64_t)(lane >> 4) * a.ks_sb + row] =
+            __uint_as_float((uint32_t)(k + 127) << 23);
+    } else {
+      *(i32x4*)(a.kv_nope + (int64_t)pg * a.kv_sp + (int64_t)row * a.kv_st + 8 * lane) = v;
+    }
     if (lane < 8) {
       const i32x4 r = *(const i32x4*)(src + kRopeOff + 8 * lane);
       *(i32x4*)(a.kv_rope + (int64_t)pg * a.kr_sp + (int64_t)row * a.kr_st + 8 * lane) = r;
@@ -1153,15 +1454,23 @@ int64_t ws_lse_bytes(int64_t slots, int64_t rows) {
   return ((slots * rows * 4) + 255) / 256 * 256;
 }
 
-template <int DT, int NW, int HT, int NS, bool WS>
+template <int DT, int NW, int HT, int NS, bool WS, bool KV8 = false>
 hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) {
-  hipLaunchKernelGGL((mla::mla_splitkv_kernel<DT, NW, HT, NS, WS>), dim3(kp.num_parts, head_blocks),
+  hipLaunchKernelGGL((mla::mla_splitkv_kernel<DT, NW, HT, NS, WS, KV8>), dim3(kp.num_parts, head_blocks),
                      dim3(NW * 64), 0, st, kp);
   return hipGetLastError();
 }
 
 template <int DT>
 hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blocks, hipStream_t st) {
+  if constexpr (DT == MLA_DTYPE_BF16) {
+    if (kp.kv_scale != nullptr) {  // fp8 latent cache
+      if (v.ws) return launch_main<DT, 4, 1, 1, true, true>(kp, head_blocks, st);
+      if (v.nw == 1) return launch_main<DT, 1, 2, 1, false, true>(kp, head_blocks, st);
+      if (v.ht == 1) return launch_main<DT, 4, 1, 4, false, true>(kp, head_blocks, st);
+      return launch_main<DT, 4, 2, 3, false, true>(kp, head_blocks, st);
+    }
+  }
   if (v.ws) return launch_main<DT, 4, 1, 1, true>(kp, head_blocks, st);
   if (v.nw == 1) return launch_main<DT, 1, 2, 1, false>(kp, head_blocks, st);
   if (v.ht == 1) return launch_main<DT, 4, 1, 4, false>(kp, head_blocks, st);
@@ -1205,6 +1514,17 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
       a->o_stride_b < 0 || a->o_stride_s < 0 || a->o_stride_h < 0)
     return fail(MLA_ERR_INVALID, "out must be 8-byte aligned with strides multiples of 4 elements");
   if (a->num_parts < 1) return fail(MLA_ERR_INVALID, "num_parts must be >= 1");
+  if ((a->kv_format != MLA_KV_NATIVE && a->kv_format != MLA_KV_FP8_E4M3) || a->kv_reserved != 0)
+    return fail(MLA_ERR_INVALID, "kv_format must be MLA_KV_NATIVE or MLA_KV_FP8_E4M3 (kv_reserved 0)");
+  if (a->kv_format == MLA_KV_FP8_E4M3) {
+    if (a->dtype != MLA_DTYPE_BF16) return fail(MLA_ERR_UNSUPPORTED, "the fp8 cache is read with bf16 queries");
+    if (!a->block_table) return fail(MLA_ERR_UNSUPPORTED, "the fp8 cache is paged only");
+    if (a->kv_stride_page % 16 || a->kv_stride_tok % 16)
+      return fail(MLA_ERR_INVALID, "fp8 latent strides must be multiples of 16 bytes");
+    if (!a->kv_scale || !aligned(a->kv_scale, 16) || a->kv_scale_stride_page < 0 ||
+        a->kv_scale_stride_blk < 0 || a->kv_scale_stride_page % 4 || a->kv_scale_stride_blk % 4)
+      return fail(MLA_ERR_INVALID, "kv_scale must be 16-byte aligned with non-negative strides, multiples of 4 floats");
+  }
   *need_ws = mla_workspace_bytes(a->batch, a->s_q, a->heads_q, a->num_parts);
   if (a->workspace == nullptr || a->workspace_bytes < *need_ws)
     return fail(MLA_ERR_WORKSPACE, "workspace missing or smaller than mla_workspace_bytes()");
@@ -1222,6 +1542,8 @@ mla::KParams make_params(const mla_decode_args* a) {
   k.kv_rope = (const uint16_t*)a->kv_rope;
   k.kv_sp = a->kv_stride_page; k.kv_st = a->kv_stride_tok; k.kv_sb = a->kv_stride_batch;
   k.kr_sp = a->kv_rope_stride_page; k.kr_st = a->kv_rope_stride_tok; k.kr_sb = a->kv_rope_stride_batch;
+  k.kv_scale = a->kv_format == MLA_KV_FP8_E4M3 ? a->kv_scale : nullptr;
+  k.ks_sp = a->kv_scale_stride_page; k.ks_sb = a->kv_scale_stride_blk;
   k.block_table = a->block_table;
   k.bt_stride = a->block_table_stride;
   k.num_blocks = a->num_blocks;
@@ -1479,6 +1801,17 @@ int mla_kv_append(const mla_kv_append_args* a, void* stream) {
     if (v < 0 || v % 8) return fail(MLA_ERR_INVALID, "strides must be non-negative multiples of 8 elements");
   if (a->block_table_stride < 1 || a->max_pages < 1 || a->num_blocks < 1)
     return fail(MLA_ERR_INVALID, "block_table_stride, max_pages and num_blocks must be >= 1");
+  if ((a->kv_format != MLA_KV_NATIVE && a->kv_format != MLA_KV_FP8_E4M3) || a->kv_reserved != 0)
+    return fail(MLA_ERR_INVALID, "kv_format must be MLA_KV_NATIVE or MLA_KV_FP8_E4M3 (kv_reserved 0)");
+  const bool kv8 = a->kv_format == MLA_KV_FP8_E4M3;
+  if (kv8) {
+    if (a->dtype != MLA_DTYPE_BF16) return fail(MLA_ERR_UNSUPPORTED, "the fp8 cache takes bf16 tokens");
+    if (a->kv_stride_page % 16 || a->kv_stride_tok % 16)
+      return fail(MLA_ERR_INVALID, "fp8 latent strides must be multiples of 16 bytes");
+    if (!a->kv_scale || !aligned(a->kv_scale, 16) || a->kv_scale_stride_page < 0 ||
+        a->kv_scale_stride_blk < 0 || a->kv_scale_stride_page % 4 || a->kv_scale_stride_blk % 4)
+      return fail(MLA_ERR_INVALID, "kv_scale must be 16-byte aligned with non-negative strides, multiples of 4 floats");
+  }
   mla::AppendParams k{};
   k.kv_new = (const uint16_t*)a->kv_new;
   k.n_sb = a->new_stride_b; k.n_st = a->new_stride_t;
@@ -1490,6 +1823,9 @@ int mla_kv_append(const mla_kv_append_args* a, void* stream) {
   k.batch = a->batch; k.n_new = a->n_new;
   k.seqlens = a->cache_seqlens;
   k.status = a->status;
+  k.kv8 = kv8 ? 1 : 0;
+  k.kv_scale = a->kv_scale;
+  k.ks_sp = a->kv_scale_stride_page; k.ks_sb = a->kv_scale_stride_blk;
   hipLaunchKernelGGL(mla::mla_kv_append_kernel, dim3((a->batch + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, k);
   const hipError_t e = hipGetLastError();

@@ -20,7 +20,7 @@ and the fp8 append implement, so that their results can be checked:
   * ``dequantize_pages`` -- the bf16-equivalent [num_blocks, 64, 576] cache the fp8 decode
     must agree with; the decode oracle is then ``mla_ref.decode_paged`` on it.
 
-Pinning (tests/test_oracle.py): ``e4m3_decode`` against the code table's closed forms and
+Pinning (tests/test_oracle_fp8.py): ``e4m3_decode`` against the code table's closed forms and
 torch's ``float8_e4m3fn`` view; ``e4m3_encode`` against torch's ``float8_e4m3fn`` cast
 (a library routine, round-to-nearest-even) on every bf16 bit pattern in range, and the
 scale rule against a float64 brute force.
@@ -38,15 +38,24 @@ NBLK = LATENT // BLOCK
 PAGE = 64
 
 
-def e4m3_decode(codes: np.ndarray) -> np.ndarray:
-    """uint8 codes -> float32 values (NaN for 0x7F / 0xFF)."""
-    c = np.asarray(codes, dtype=np.uint8).astype(np.int32)
+def _e4m3_value(c: np.ndarray) -> np.ndarray:
+    """The value of each code from its fields: sign, 4-bit exponent (bias 7), 3-bit mantissa;
+    exponent 0 is subnormal (m/8 * 2^-6); S.1111.111 is NaN."""
+    c = c.astype(np.int32)
     sign = np.where(c & 0x80, -1.0, 1.0)
     e = (c >> 3) & 0xF
     m = c & 7
     val = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.exp2(e - 7.0))
     val = np.where((e == 15) & (m == 7), np.nan, val)
     return (sign * val).astype(np.float32)
+
+
+_E4M3_TABLE = _e4m3_value(np.arange(256))
+
+
+def e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """uint8 codes -> float32 values (NaN for 0x7F / 0xFF), through the 256-entry table."""
+    return _E4M3_TABLE[np.asarray(codes, dtype=np.uint8)]
 
 
 def e4m3_encode(x: np.ndarray) -> np.ndarray:

@@ -4,6 +4,8 @@ come back as nonzero statuses with messages (validation runs before any HIP call
 import ctypes
 import os
 import random
+import shutil
+import subprocess
 import re
 
 import pytest
@@ -37,11 +39,27 @@ def test_exports_every_declared_symbol(lib):
     assert lib.mla_last_error() is not None
 
 
-def test_struct_layout_matches_header():
-    # 8 int/float fields, then pointers / int64s; spot-check offsets the C side relies on
-    assert MlaDecodeArgs.q_nope.offset == 32
-    assert ctypes.sizeof(MlaDecodeArgs) % 8 == 0
-    assert MlaDecodeArgs.workspace_bytes.offset == ctypes.sizeof(MlaDecodeArgs) - 8
+def _c_layout(tmp_path, struct, fields):
+    """sizeof and offsetof of `fields` as the C compiler lays out `struct` from the header."""
+    src = tmp_path / "layout.c"
+    body = "".join(f'  printf("%zu\\n", offsetof({struct}, {f}));\n' for f in fields)
+    src.write_text(f'#include <stddef.h>\n#include <stdio.h>\n#include "mla_decode_amd.h"\n'
+                   f'int main(void) {{\n  printf("%zu\\n", sizeof({struct}));\n{body}  return 0;\n}}\n')
+    exe = tmp_path / "layout"
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    subprocess.run(["gcc", "-std=c99", "-I", inc, "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    return [int(v) for v in out]
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc to lay out the header's structs")
+@pytest.mark.parametrize("cls,name", [(MlaDecodeArgs, "mla_decode_args"),
+                                      (_lib.MlaKvAppendArgs, "mla_kv_append_args")])
+def test_struct_layout_matches_header(tmp_path, cls, name):
+    fields = [f for f, _ in cls._fields_]
+    c = _c_layout(tmp_path, name, fields)
+    assert c[0] == ctypes.sizeof(cls)
+    assert c[1:] == [getattr(cls, f).offset for f in fields]
 
 
 def test_split_plan_matches_reference_rule(lib):
@@ -154,6 +172,27 @@ def test_decode_rejects_bad_args(lib, field, value, code, needle):
     assert needle in lib.mla_last_error()
     with pytest.raises(_lib.MlaError):
         _lib.check("mla_decode_fwd", rc)
+
+
+@pytest.mark.parametrize("changes,code,needle", [
+    (dict(kv_format=2), 1, b"kv_format"),
+    (dict(kv_reserved=1), 1, b"kv_format"),
+    (dict(kv_format=1, dtype=1), 4, b"bf16"),
+    (dict(kv_format=1, block_table=None), 4, b"paged"),
+    (dict(kv_format=1), 1, b"kv_scale"),                                   # no scale array
+    (dict(kv_format=1, kv_scale=(1 << 20) + 4), 1, b"kv_scale"),            # misaligned
+    (dict(kv_format=1, kv_scale=1 << 20, kv_scale_stride_blk=65), 1, b"kv_scale"),
+    (dict(kv_format=1, kv_scale=1 << 20, kv_stride_tok=520), 1, b"16 bytes"),
+    (dict(kv_format=1, kv_scale=1 << 20, kv_scale_stride_page=256, kv_scale_stride_blk=64,
+          kv_stride_tok=512, kv_stride_page=32768), 2, b"workspace"),      # valid up to the workspace
+])
+def test_decode_rejects_bad_fp8_args(lib, changes, code, needle):
+    a = _valid_args()
+    for k, v in changes.items():
+        setattr(a, k, v)
+    rc = lib.mla_decode_fwd(ctypes.byref(a), None)
+    assert rc == code
+    assert needle in lib.mla_last_error()
 
 
 def test_metadata_rejects_bad_args(lib):
