@@ -39,6 +39,9 @@ def parse():
     ap.add_argument("--append", action="store_true",
                     help="measure the paged KV-cache append (mla_kv_append) at every config's "
                          "batch and s_q instead of the decode; one JSON line per config")
+    ap.add_argument("--kv-fp8", action="store_true",
+                    help="measure the decode over the fp8 (e4m3) latent cache at every config (bf16 "
+                         "queries); one JSON line per config")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain MIB-MiB device copy 3x (scale for FETCH/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -89,15 +92,23 @@ def settle_clocks(fn, stream, seconds=0.25):
         n = min(n * 2, 256)
 
 
-def measure(cfg_name, steps, warmup):
+FP8_TOKEN_BYTES = 512 + 64 * 2 + 4 * 4  # e4m3 latent codes, bf16 rope, four fp32 block scales
+
+
+def measure(cfg_name, steps, warmup, kv_fp8=False):
+    import dataclasses
+
     import torch
     from mlc_decode_amd import _lib
-    from mlc_decode_amd.api import flash_mla_with_kvcache, get_mla_metadata
+    from mlc_decode_amd.api import flash_mla_with_kvcache, get_mla_metadata, quantize_kv_cache
     from mlc_decode_amd.inputs import CONFIGS, algorithmic_bytes, algorithmic_flops, make_inputs
 
     cfg = CONFIGS[cfg_name]
+    if kv_fp8 and cfg.dtype != torch.bfloat16:
+        cfg = dataclasses.replace(cfg, dtype=torch.bfloat16)  # the fp8 cache takes bf16 queries
     cpu_inp = make_inputs(cfg, seed=0)
     inp = cpu_inp.to("cuda:0")
+    kv = quantize_kv_cache(inp.kv_cache) if kv_fp8 else inp.kv_cache
     B, s_q, H = cfg.batch, cfg.s_q, cfg.heads
     stream = torch.cuda.current_stream()
     forced = cfg.num_splits or 0
@@ -109,13 +120,13 @@ def measure(cfg_name, steps, warmup):
     from mlc_decode_amd._lib import check
     from mlc_decode_amd.api import make_decode_args
     lib = _lib.load()
-    args, _, _, keep = make_decode_args(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+    args, _, _, keep = make_decode_args(inp.q, kv, inp.block_table, inp.cache_seqlens,
                                         sched, splits, inp.sm_scale, inp.causal, out, lse)
     ap = ctypes.byref(args)
     sp = stream.cuda_stream
 
     def call():  # the public call path, validation and all
-        flash_mla_with_kvcache(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, 512,
+        flash_mla_with_kvcache(inp.q, kv, inp.block_table, inp.cache_seqlens, 512,
                                sched, splits, softmax_scale=inp.sm_scale, causal=inp.causal,
                                out=out, lse=lse)
 
@@ -131,6 +142,8 @@ def measure(cfg_name, steps, warmup):
     del keep
 
     nbytes = algorithmic_bytes(cpu_inp.cache_seqlens, B, s_q, H, 2)
+    if kv_fp8:  # KV at FP8_TOKEN_BYTES per cached token instead of 576 bf16 values
+        nbytes -= int(cpu_inp.cache_seqlens.sum()) * (576 * 2 - FP8_TOKEN_BYTES)
     flops = algorithmic_flops(cpu_inp.cache_seqlens, s_q, H, cfg.causal)
     t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
     t_mfma = flops / (MFMA_PEAK_TFLOPS * 1e12)
@@ -230,6 +243,18 @@ def main():
     if args.append:
         for name in ("C1", "C2", "C3", "C4", "C5"):
             print(json.dumps(measure_append(name, args.steps)), flush=True)
+        return
+    if args.kv_fp8:
+        for name in ("C1", "C2", "C3", "C4", "C5"):
+            mm = measure(name, args.steps, args.warmup, kv_fp8=True)
+            frac = (mm["gbs"] / HBM_PEAK_GBS) if mm["bound"] == "hbm" else (mm["tflops"] / MFMA_PEAK_TFLOPS)
+            print(json.dumps({"op": "decode_fp8_cache", "config": name, "us_call": round(mm["ms_call"] * 1e3, 2),
+                              "us_main": round(mm["ms_main"] * 1e3, 2),
+                              "us_combine": round(mm["ms_combine"] * 1e3, 2),
+                              "algorithmic_bytes": mm["nbytes"], "tbps": round(mm["gbs"] / 1e3, 3),
+                              "tflops": round(mm["tflops"], 1), "bound": mm["bound"],
+                              "roofline_frac": round(frac, 4), "parts": mm["parts"],
+                              "splits": mm["n_splits"]}), flush=True)
         return
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20)
