@@ -55,6 +55,9 @@ extern "C" {
 /* Per-split overhead, in pages, of the default (min-payload) tile schedule. */
 #define MLA_DEFAULT_SPLIT_OVERHEAD 3
 
+/* Longest top-k index list of the sparse decode. */
+#define MLA_SPARSE_MAX_TOPK 2048
+
 /* KV cache formats (mla_decode_args.kv_format, mla_kv_append_args.kv_format). */
 #define MLA_KV_NATIVE 0   /* latent and rope in the query dtype */
 #define MLA_KV_FP8_E4M3 1 /* latent as OCP e4m3 codes with power-of-two scales (below) */
@@ -128,6 +131,16 @@ typedef struct mla_decode_args {
   int32_t kv_reserved; /* must be 0 */
   const float* kv_scale;
   int64_t kv_scale_stride_page, kv_scale_stride_blk;
+
+  /* Sparse (top-k) decode when indices != NULL (s_q == 1, native cache): the keys of sequence b
+   * are the pool tokens indices[b * indices_stride + j], j < topk (1 .. MLA_SPARSE_MAX_TOPK),
+   * token id = page * 64 + row of the paged cache (kv_nope / kv_rope with the page strides);
+   * an index < 0 or >= num_blocks * 64 names no key.  block_table and cache_seqlens are not
+   * read; the schedule (tile_sched / num_splits) must be the one mla_get_metadata gives for
+   * sequence lengths all equal to topk. */
+  const int32_t* indices;
+  int32_t indices_stride;
+  int32_t topk;
 } mla_decode_args;
 
 /* Library version (MLA_DECODE_AMD_VERSION). */

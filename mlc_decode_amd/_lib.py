@@ -18,6 +18,7 @@ MLA_SCHED_WORDS = 8
 MLA_DEFAULT_SPLIT_OVERHEAD = 3  # pages; the default schedule's per-split overhead
 MLA_KV_NATIVE = 0
 MLA_KV_FP8_E4M3 = 1
+MLA_SPARSE_MAX_TOPK = 2048
 MLA_DIM_QK = 576
 MLA_DIM_V = 512
 MLA_PAGE_TOKENS = 64
@@ -90,6 +91,9 @@ class MlaDecodeArgs(ctypes.Structure):
         ("kv_scale", _vp),
         ("kv_scale_stride_page", _i64),
         ("kv_scale_stride_blk", _i64),
+        ("indices", _vp),
+        ("indices_stride", _i32),
+        ("topk", _i32),
     ]
 
 

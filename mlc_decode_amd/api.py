@@ -83,7 +83,7 @@ def kernel_variant(rows: int) -> dict:
 
 def get_mla_metadata(cache_seqlens: torch.Tensor, num_heads_per_head_k: int, num_heads_k: int,
                      num_parts: Optional[int] = None, fixed_overhead: int = -1,
-                     forced_splits: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+                     forced_splits: int = 0, topk: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Tile schedule: ``(tile_scheduler_metadata [num_parts, 8] int32, num_splits [B+1] int32)``.
 
     ``num_heads_per_head_k`` is ``s_q * h_q // h_kv`` as in the reference's call; it picks
@@ -92,9 +92,14 @@ def get_mla_metadata(cache_seqlens: torch.Tensor, num_heads_per_head_k: int, num
     ``ceil(total / parts) + fixed_overhead``; the default (``fixed_overhead < 0``) packs at the
     smallest payload that fits, with the library's overhead ``MLA_DEFAULT_SPLIT_OVERHEAD``.
     ``forced_splits > 0`` cuts every sequence into that many near-equal page ranges instead
-    (then ``num_parts = B * forced_splits``).
+    (then ``num_parts = B * forced_splits``).  ``topk`` (sparse decode): every sequence is
+    scheduled as ``topk`` keys long, whatever ``cache_seqlens`` holds.
     """
     _require_gpu(cache_seqlens, "cache_seqlens")
+    if topk is not None:
+        if not 1 <= topk <= _lib.MLA_SPARSE_MAX_TOPK:
+            raise ValueError(f"topk must be in [1, {_lib.MLA_SPARSE_MAX_TOPK}]")
+        cache_seqlens = torch.full((cache_seqlens.numel(),), topk, dtype=torch.int32, device=cache_seqlens.device)
     if num_heads_k != 1:
         raise ValueError("only one latent KV head (num_heads_k == 1) is supported")
     if cache_seqlens.dtype != torch.int32 or cache_seqlens.dim() != 1:
@@ -175,10 +180,10 @@ def _split_kv(kv_cache) -> Tuple[torch.Tensor, torch.Tensor]:
     return kv_cache[..., :MLA_DIM_V], kv_cache[..., MLA_DIM_V:]
 
 
-def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
-                     cache_seqlens: torch.Tensor, sched: torch.Tensor, splits: torch.Tensor,
+def make_decode_args(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tensor],
+                     cache_seqlens: Optional[torch.Tensor], sched: torch.Tensor, splits: torch.Tensor,
                      sm_scale: float, causal: bool, out: Optional[torch.Tensor] = None,
-                     lse: Optional[torch.Tensor] = None):
+                     lse: Optional[torch.Tensor] = None, indices: Optional[torch.Tensor] = None):
     """Validate a paged decode and fill the C ``mla_decode_args`` for it.
 
     Returns ``(args, out, lse, keep)``; ``keep`` holds the tensors the args point into and
@@ -203,13 +208,30 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
                 raise ValueError("kv cache dtype must match q")
             if t.dim() != 4 or t.shape[1] != _lib.MLA_PAGE_TOKENS or t.shape[2] != 1 or t.stride(-1) != 1:
                 raise ValueError("kv cache must be [num_blocks, 64, 1, D] with unit stride in D")
-    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
-        raise ValueError("block_table must be a [B, P] int32 tensor with unit column stride")
-    if cache_seqlens.dtype != torch.int32 or cache_seqlens.dim() != 1:
-        raise ValueError("cache_seqlens must be a 1-D int32 tensor")
     B, s_q, H, _ = q.shape
-    if block_table.shape[0] != B or cache_seqlens.shape[0] != B or splits.numel() != B + 1:
-        raise ValueError("batch size of q, block_table, cache_seqlens and num_splits disagree")
+    if indices is not None:  # sparse: keys named by index, no page table or lengths
+        _require_gpu(indices, "indices")
+        if fp8:
+            raise ValueError("the sparse decode reads the 16-bit cache")
+        if s_q != 1:
+            raise ValueError("the sparse decode takes s_q == 1")
+        if indices.dim() == 3:
+            if indices.shape[1] != 1:
+                raise ValueError("indices must be [B, 1, topk] (s_q == 1)")
+            indices = indices[:, 0]
+        if indices.dtype != torch.int32 or indices.dim() != 2 or indices.shape[0] != B or indices.stride(1) != 1:
+            raise ValueError("indices must be an int32 [B, topk] (or [B, 1, topk]) tensor, unit stride in topk")
+        if not 1 <= indices.shape[1] <= _lib.MLA_SPARSE_MAX_TOPK:
+            raise ValueError(f"topk must be in [1, {_lib.MLA_SPARSE_MAX_TOPK}]")
+        if splits.numel() != B + 1:
+            raise ValueError("batch size of q and num_splits disagree")
+    else:
+        if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+            raise ValueError("block_table must be a [B, P] int32 tensor with unit column stride")
+        if cache_seqlens.dtype != torch.int32 or cache_seqlens.dim() != 1:
+            raise ValueError("cache_seqlens must be a 1-D int32 tensor")
+        if block_table.shape[0] != B or cache_seqlens.shape[0] != B or splits.numel() != B + 1:
+            raise ValueError("batch size of q, block_table, cache_seqlens and num_splits disagree")
     if q.stride(-1) != 1:
         raise ValueError("q must have unit stride in its last dim")
     if out is None:
@@ -220,7 +242,7 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
         raise ValueError("lse must be a contiguous fp32 [B, H, s_q] tensor")
     if out.shape != (B, s_q, H, MLA_DIM_V) or out.dtype != q.dtype or out.stride(-1) != 1:
         raise ValueError("out must be [B, s_q, H, 512] in q's dtype with unit last stride")
-    seqlens = cache_seqlens.contiguous()
+    seqlens = cache_seqlens.contiguous() if cache_seqlens is not None else None
     sched = sched.contiguous()
     splits = splits.contiguous()
     num_parts = sched.shape[0]
@@ -245,10 +267,16 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
     if fp8:
         a.kv_scale = scale.data_ptr()
         a.kv_scale_stride_page, a.kv_scale_stride_blk = scale.stride(0), scale.stride(1)
-    a.block_table = block_table.data_ptr()
-    a.block_table_stride = block_table.stride(0)
+    if indices is not None:
+        a.indices = indices.data_ptr()
+        a.indices_stride, a.topk = indices.stride(0), indices.shape[1]
+        a.block_table, a.block_table_stride = None, 0
+        a.kv_stride_batch = a.kv_rope_stride_batch = 0
+    else:
+        a.block_table = block_table.data_ptr()
+        a.block_table_stride = block_table.stride(0)
     a.num_parts = num_parts
-    a.cache_seqlens = seqlens.data_ptr()
+    a.cache_seqlens = seqlens.data_ptr() if seqlens is not None else None
     a.tile_sched = sched.data_ptr()
     a.num_splits = splits.data_ptr()
     a.out = out.data_ptr()
@@ -256,14 +284,14 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
     a.lse = lse.data_ptr()
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws_bytes
-    keep = (q, latent, rope, scale, block_table, seqlens, sched, splits, out, lse, ws)
+    keep = (q, latent, rope, scale, block_table, seqlens, sched, splits, out, lse, ws, indices)
     return a, out, lse, keep
 
 
 def _decode(q, kv_cache, block_table, cache_seqlens, sched, splits, sm_scale, causal,
-            out=None, lse=None):
+            out=None, lse=None, indices=None):
     a, out, lse, keep = make_decode_args(q, kv_cache, block_table, cache_seqlens, sched, splits,
-                                         sm_scale, causal, out, lse)
+                                         sm_scale, causal, out, lse, indices)
     check("mla_decode_fwd", _lib.load().mla_decode_fwd(ctypes.byref(a), _stream_ptr(q.device)))
     del keep
     return out, lse
@@ -273,17 +301,23 @@ def flash_mla_with_kvcache(q: torch.Tensor, k_cache, block_table: torch.Tensor,
                            cache_seqlens: torch.Tensor, head_dim_v: int,
                            tile_scheduler_metadata: torch.Tensor, num_splits: torch.Tensor,
                            softmax_scale: Optional[float] = None, causal: bool = False,
-                           out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+                           out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+                           indices: Optional[torch.Tensor] = None):
     """Paged decode with a precomputed schedule -> ``(out [B,s_q,H,512], lse [B,H,s_q])``.
 
     Same call shape as the reference's use of FlashMLA (handmade/bench_metax_flashmla.py:33-35).
+    ``indices`` (int32 ``[B, 1, topk]``, s_q = 1) selects the sparse decode: the keys of sequence
+    b are the pool tokens ``indices[b, 0, j]`` (page id * 64 + row; -1 or any id outside the
+    cache names no key), ``block_table`` / ``cache_seqlens`` are not read and the schedule must
+    come from ``get_mla_metadata(..., topk=topk)``.  No counterpart in the reference's Python
+    path: MetaX FlashMLA ships such a kernel (docs/flashmla_metax_analysis.md:43).
     """
     if head_dim_v != MLA_DIM_V:
         raise ValueError(f"head_dim_v must be {MLA_DIM_V}")
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** -0.5
     return _decode(q, k_cache, block_table, cache_seqlens, tile_scheduler_metadata, num_splits,
-                   softmax_scale, causal, out, lse)
+                   softmax_scale, causal, out, lse, indices)
 
 
 def mla_decode_with_kvcache(q: torch.Tensor, kv_cache, block_table: torch.Tensor,

@@ -86,6 +86,11 @@ struct KParams {
   // power-of-two scales, [page][128-dim block][token] with strides ks_sp, ks_sb (floats)
   const float* kv_scale;
   int64_t ks_sp, ks_sb;
+  // sparse (top-k) decode only: the keys of sequence b are the pool tokens
+  // indices[b * idx_stride + j], j < topk (page id * 64 + row; out of range = no key)
+  const int32_t* indices;
+  int32_t idx_stride, topk;
+  int64_t pool_tokens;
   int32_t batch, s_q, heads, rows, causal, num_parts;
   float scale_log2;  // sm_scale * log2(e)
 };
@@ -205,6 +210,16 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
       : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
       : "memory", "m0");
 }
+// The same copy from a per-lane 64-bit address (the sparse path: every token row has its own
+// page).
+__device__ __forceinline__ void dma16_lane(const void* addr, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %0, off nt"
+      :
+      : "v"(addr), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+      : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Workgroup barrier for LDS hand-off only.  Each wave has already waited for its own DMA
@@ -265,6 +280,36 @@ __device__ __forceinline__ void issue_stage(uint8_t LDS_AS* slot, const uint16_t
     for (int sg = 0; sg < 8; ++sg)
       dma16((const char*)nope_base + 128 * sg, on, (uint32_t)(uintptr_t)(dst + sg * 1024));
     dma16(rope_base, orp, (uint32_t)(uintptr_t)(dst + 8 * 1024));
+  }
+}
+
+// Sparse (top-k) decode: the same stage layout, each token row fetched from its own pool token
+// (idx_stage[r] = page * 64 + row); rows past the list's end re-read its last row, and an index
+// outside the pool reads pool token 0 (both are masked by the caller).
+constexpr int kSparseMaxTopk = 2048;
+template <int NL>
+__device__ __forceinline__ void issue_stage_sparse(uint8_t LDS_AS* slot, const uint16_t* nope_pool,
+                                                   const uint16_t* rope_pool,
+                                                   const int32_t LDS_AS* idx_stage, int valid_rows,
+                                                   int64_t kv_sp, int64_t kv_st, int64_t kr_sp,
+                                                   int64_t kr_st, int64_t pool_tokens, int wave,
+                                                   int lane) {
+  static_assert(NL == 1 || NL == 4, "stage loads are split over one or four waves");
+#pragma unroll
+  for (int qi = 0; qi < 4 / NL; ++qi) {
+    const int q = NL == 1 ? qi : wave;  // uniform
+    const int r = 8 * q + (lane >> 3);
+    const int t = r < valid_rows ? r : valid_rows - 1;
+    int64_t idx = idx_stage[t];
+    if (idx < 0 || idx >= pool_tokens) idx = 0;
+    const int64_t pg = idx >> 6, rw = idx & 63;
+    const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((q & 1) << 3) | (lane >> 3))) << 4);
+    const char* nrow = (const char*)(nope_pool + pg * kv_sp + rw * kv_st) + cl;
+    const char* rrow = (const char*)(rope_pool + pg * kr_sp + rw * kr_st) + cl;
+    uint8_t LDS_AS* dst = slot + q * 9 * 1024;
+#pragma unroll
+    for (int sg = 0; sg < 8; ++sg) dma16_lane(nrow + 128 * sg, (uint32_t)(uintptr_t)(dst + sg * 1024));
+    dma16_lane(rrow, (uint32_t)(uintptr_t)(dst + 8 * 1024));
   }
 }
 
@@ -388,10 +433,12 @@ constexpr int waves_per_simd(int nw, int ht, int nstage, bool ws) {
 // KV8: the latent cache holds OCP e4m3 codes with power-of-two scales per token and 128-dim
 // block (bf16 queries and rope); K fragments are converted to bf16 with their scale on the way
 // from LDS to the MFMA, V^T fragments without it, and the scales of V are folded into P^T.
-template <int DT, int NW, int HT, int NSTAGE, bool WS, bool KV8>
+// SPARSE: the keys of a sequence are the top-k pool tokens its index list names (s_q = 1).
+template <int DT, int NW, int HT, int NSTAGE, bool WS, bool KV8, bool SPARSE = false>
 __global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW > 0
                                           ? waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW : 1)
 void mla_splitkv_kernel(KParams p) {
+  static_assert(!(SPARSE && KV8), "the sparse path reads the 16-bit cache");
   static_assert(NW == 1 || NW == 4, "one or four waves per workgroup");
   static_assert(!WS || NSTAGE == 1, "wave-split workgroups give each wave a one-stage slot");
   static_assert(!KV8 || DT == MLA_DTYPE_BF16, "the fp8 cache is read with bf16 queries");
@@ -412,6 +459,8 @@ void mla_splitkv_kernel(KParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSmem];
   // wave-split merge words: (row max, row sum) per wave and row
   __shared__ float merge_sh[WS ? NW : 1][2][16];
+  // sparse: the pool-token indices of the current segment
+  __shared__ int32_t idx_sh[SPARSE ? kSparseMaxTopk : 1];
   // "score above reference" words, one per stage modulo 4.  A wave whose stage-k scores exceed
   // the reference stores 1 into over_sh[k % 4] (a wave-uniform branch, all lanes storing the
   // same value); every wave reads the word after the next barrier; wave 0 clears it two
@@ -474,7 +523,7 @@ void mla_splitkv_kernel(KParams p) {
 #pragma unroll 1
   for (; b < p.batch; ++b, page = 0, split = 0) {
     if (!(b < end_b || (b == end_b && page < end_page))) break;
-    const int L = p.seqlens[b] > 0 ? p.seqlens[b] : 0;
+    const int L = SPARSE ? p.topk : (p.seqlens[b] > 0 ? p.seqlens[b] : 0);
     const int np = pages_of(L);
     const int stop = (b == end_b) ? end_page : np;
     const int st_begin = 2 * page;
@@ -509,6 +558,16 @@ void mla_splitkv_kernel(KParams p) {
       }
     }
     const int lmin = L - (p.causal ? p.s_q - 1 : 0);  // every row sees tokens < lmin
+    if constexpr (SPARSE) {
+      // the segment's index list into LDS (every wave of the workgroup runs this segment; the
+      // previous segment's readers are past its final barrier)
+      const int tok0 = st_begin * kStageTok;
+      int ntok = L - tok0;
+      ntok = ntok < nst * kStageTok ? ntok : nst * kStageTok;
+      for (int i = threadIdx.x; i < ntok; i += NW * 64) idx_sh[i] = p.indices[(int64_t)b * p.idx_stride + tok0 + i];
+      wait_lgkm0();
+      lds_barrier();
+    }
 
     f32x4 o[kDimTiles][HT];
     float m_ref[HT], l_part[HT];
@@ -517,7 +576,7 @@ void mla_splitkv_kernel(KParams p) {
     auto load_page_ids = [&](int first) __attribute__((always_inline)) {
       // lane i holds the page id of page (first + i); ids are clamped into the pool
       pbase = first;
-      if (paged) {
+      if (paged && !SPARSE) {
         // branch-free: every lane loads an in-bounds entry (row b always has column 0)
         const int last = np > 0 ? np - 1 : 0;
         const int pi = pbase + lane < last ? pbase + lane : last;
@@ -528,6 +587,14 @@ void mla_splitkv_kernel(KParams p) {
 
     auto issue = [&](int k) __attribute__((always_inline)) {
       const int st = st_begin + k;
+      if constexpr (SPARSE) {
+        const int left = L - st * kStageTok;
+        issue_stage_sparse<NL>(ring + (k % NSTAGE) * kSB, p.kv_nope, p.kv_rope,
+                               (const int32_t LDS_AS*)idx_sh + k * kStageTok,
+                               left < kStageTok ? left : kStageTok, p.kv_sp, p.kv_st, p.kr_sp, p.kr_st,
+                               p.pool_tokens, NL == 1 ? 0 : wave, lane);
+        return;
+      }
       if constexpr (KV8) {  // paged only (checked by the host)
         const int pidx = st >> 1;
         if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
@@ -856,8 +923,25 @@ void mla_splitkv_kernel(KParams p) {
           else v_prefetch(k, vf);
         }
 
+        // ---- sparse: mask the stage's tokens whose index is past the list or outside the pool
+        if constexpr (SPARSE) {
+          const int left = L - st * kStageTok;
+          bool valid = false;
+          if (lane < kStageTok && lane < left) {
+            const int v = ((const int32_t LDS_AS*)idx_sh)[k * kStageTok + lane];
+            valid = v >= 0 && (int64_t)v < p.pool_tokens;
+          }
+          const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(valid);
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (!((vmask >> (16 * tt + 4 * g + r)) & 1u)) acc[ht][tt][r] = -INFINITY;
+        }
         // ---- mask tokens past each row's limit (sequence tail / causal)
-        if (st * kStageTok + kStageTok > lmin) {
+        if (!SPARSE && st * kStageTok + kStageTok > lmin) {
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) {
             // token 16*tt + 4*g + r of the stage is visible iff 16*tt + r < rel; the empty
@@ -1454,15 +1538,21 @@ int64_t ws_lse_bytes(int64_t slots, int64_t rows) {
   return ((slots * rows * 4) + 255) / 256 * 256;
 }
 
-template <int DT, int NW, int HT, int NS, bool WS, bool KV8 = false>
+template <int DT, int NW, int HT, int NS, bool WS, bool KV8 = false, bool SPARSE = false>
 hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) {
-  hipLaunchKernelGGL((mla::mla_splitkv_kernel<DT, NW, HT, NS, WS, KV8>), dim3(kp.num_parts, head_blocks),
+  hipLaunchKernelGGL((mla::mla_splitkv_kernel<DT, NW, HT, NS, WS, KV8, SPARSE>), dim3(kp.num_parts, head_blocks),
                      dim3(NW * 64), 0, st, kp);
   return hipGetLastError();
 }
 
 template <int DT>
 hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blocks, hipStream_t st) {
+  if (kp.indices != nullptr) {  // sparse (top-k) decode
+    if (v.ws) return launch_main<DT, 4, 1, 1, true, false, true>(kp, head_blocks, st);
+    if (v.nw == 1) return launch_main<DT, 1, 2, 1, false, false, true>(kp, head_blocks, st);
+    if (v.ht == 1) return launch_main<DT, 4, 1, 4, false, false, true>(kp, head_blocks, st);
+    return launch_main<DT, 4, 2, 3, false, false, true>(kp, head_blocks, st);
+  }
   if constexpr (DT == MLA_DTYPE_BF16) {
     if (kp.kv_scale != nullptr) {  // fp8 latent cache
       if (v.ws) return launch_main<DT, 4, 1, 1, true, true>(kp, head_blocks, st);
@@ -1486,8 +1576,8 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
     return fail(MLA_ERR_INVALID, "dtype must be MLA_DTYPE_BF16 or MLA_DTYPE_F16");
   if ((int64_t)a->s_q * a->heads_q > 65536) return fail(MLA_ERR_UNSUPPORTED, "s_q * heads_q exceeds 65536");
   if (!(a->sm_scale > 0.f) || !isfinite(a->sm_scale)) return fail(MLA_ERR_INVALID, "sm_scale must be finite and > 0");
-  if (!a->q_nope || !a->q_rope || !a->kv_nope || !a->kv_rope || !a->out || !a->cache_seqlens ||
-      !a->tile_sched || !a->num_splits)
+  if (!a->q_nope || !a->q_rope || !a->kv_nope || !a->kv_rope || !a->out ||
+      (!a->cache_seqlens && !a->indices) || !a->tile_sched || !a->num_splits)
     return fail(MLA_ERR_INVALID, "a required pointer is NULL");
   if (!aligned(a->q_nope, 16) || !aligned(a->q_rope, 16) || !aligned(a->kv_nope, 16) ||
       !aligned(a->kv_rope, 16))
@@ -1516,6 +1606,16 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
   if (a->num_parts < 1) return fail(MLA_ERR_INVALID, "num_parts must be >= 1");
   if ((a->kv_format != MLA_KV_NATIVE && a->kv_format != MLA_KV_FP8_E4M3) || a->kv_reserved != 0)
     return fail(MLA_ERR_INVALID, "kv_format must be MLA_KV_NATIVE or MLA_KV_FP8_E4M3 (kv_reserved 0)");
+  if (a->indices) {
+    if (a->s_q != 1) return fail(MLA_ERR_UNSUPPORTED, "the sparse decode takes s_q == 1");
+    if (a->kv_format != MLA_KV_NATIVE) return fail(MLA_ERR_UNSUPPORTED, "the sparse decode reads the 16-bit cache");
+    if (a->topk < 1 || a->topk > MLA_SPARSE_MAX_TOPK)
+      return fail(MLA_ERR_UNSUPPORTED, "topk must be in [1, MLA_SPARSE_MAX_TOPK]");
+    if (a->indices_stride < a->topk) return fail(MLA_ERR_INVALID, "indices_stride must be >= topk");
+    if (a->num_blocks < 1) return fail(MLA_ERR_INVALID, "num_blocks must be >= 1");
+    if (a->kv_stride_page < 0 || a->kv_stride_page % 8 || a->kv_rope_stride_page < 0 || a->kv_rope_stride_page % 8)
+      return fail(MLA_ERR_INVALID, "page strides must be non-negative multiples of 8 elements");
+  }
   if (a->kv_format == MLA_KV_FP8_E4M3) {
     if (a->dtype != MLA_DTYPE_BF16) return fail(MLA_ERR_UNSUPPORTED, "the fp8 cache is read with bf16 queries");
     if (!a->block_table) return fail(MLA_ERR_UNSUPPORTED, "the fp8 cache is paged only");
@@ -1544,6 +1644,10 @@ mla::KParams make_params(const mla_decode_args* a) {
   k.kr_sp = a->kv_rope_stride_page; k.kr_st = a->kv_rope_stride_tok; k.kr_sb = a->kv_rope_stride_batch;
   k.kv_scale = a->kv_format == MLA_KV_FP8_E4M3 ? a->kv_scale : nullptr;
   k.ks_sp = a->kv_scale_stride_page; k.ks_sb = a->kv_scale_stride_blk;
+  k.indices = a->indices;
+  k.idx_stride = a->indices_stride;
+  k.topk = a->topk;
+  k.pool_tokens = (int64_t)a->num_blocks * mla::kPageTokens;
   k.block_table = a->block_table;
   k.bt_stride = a->block_table_stride;
   k.num_blocks = a->num_blocks;

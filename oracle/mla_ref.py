@@ -16,6 +16,10 @@ Functions and the reference code they follow:
   * ``append_paged``       -- the paged KV-cache append (no reference counterpart: the
     reference decodes a pre-filled cache; the page/row mapping is the one ``gather``
     reads, handmade/bench_metax_flashmla.py:53-61).
+  * ``decode_sparse`` / ``dense_indices`` -- the top-k decode: the same math over the pool
+    tokens an index list names (MetaX FlashMLA's sparse kernel, docs/flashmla_metax_analysis.md:43,
+    has no source in the reference; pinned by equality with ``decode_paged`` through
+    ``dense_indices``, index-permutation invariance and the empty list).
   * ``pack_greedy`` / ``schedule_min_payload`` -- the same greedy loop at an explicit payload
     (no catch-all last part), and the smallest payload in [ceil(total/parts),
     ceil(total/parts) + f] whose packing fits (the library's default schedule).
@@ -112,6 +116,42 @@ def decode_paged(q, kv_cache, block_table, cache_seqlens, sm_scale, causal=True,
             lse[b, :, i] = torch.logsumexp(s, -1)
             out[b, i] = torch.matmul(torch.softmax(s, -1), v[:n])
     return out, lse
+
+
+def decode_sparse(q, kv_cache, indices, sm_scale, dtype=torch.float32):
+    """Sparse (top-k) decode: q [B,1,H,576], kv_cache [N,64,1,576], indices [B,1,topk] or
+    [B,topk] int -> (out [B,1,H,512], lse [B,H,1]).
+
+    The keys of sequence b are the pool tokens indices[b, j] (page * 64 + row); an index < 0 or
+    >= N * 64 names no key.  Rows with no key get out = 0 and lse = -inf.
+    """
+    B, s_q, H, _ = q.shape
+    assert s_q == 1
+    idx = indices.reshape(B, -1).to(torch.int64)
+    pool = kv_cache.reshape(-1, kv_cache.shape[-1])                        # [N*64, 576]
+    out = torch.zeros(B, 1, H, D_V, dtype=dtype)
+    lse = torch.full((B, H, 1), -math.inf, dtype=dtype)
+    for b in range(B):
+        sel = idx[b][(idx[b] >= 0) & (idx[b] < pool.shape[0])]
+        if sel.numel() == 0:
+            continue
+        k = pool[sel].to(dtype)
+        s = torch.matmul(q[b, 0].to(dtype), k.t()) * sm_scale              # [H, n]
+        lse[b, :, 0] = torch.logsumexp(s, -1)
+        out[b, 0] = torch.matmul(torch.softmax(s, -1), k[:, :D_V])
+    return out, lse
+
+
+def dense_indices(block_table, cache_seqlens, topk):
+    """The index lists that make decode_sparse equal decode_paged (s_q = 1): token t < L_b of
+    sequence b is pool token block_table[b, t // 64] * 64 + t % 64; the rest is -1."""
+    B = block_table.shape[0]
+    idx = torch.full((B, topk), -1, dtype=torch.int32)
+    for b in range(B):
+        L = min(int(cache_seqlens[b]), topk)
+        t = torch.arange(L)
+        idx[b, :L] = (block_table[b, t // PAGE].to(torch.int64) * PAGE + t % PAGE).to(torch.int32)
+    return idx
 
 
 def combine(part_o: torch.Tensor, part_lse: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:

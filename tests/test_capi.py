@@ -260,3 +260,20 @@ def test_kv_append_python_checks():
     with pytest.raises(ValueError):  # host tensors are refused: there is no CPU path
         kv_append(new, torch.zeros(4, 64, 1, 576, dtype=torch.bfloat16),
                   torch.zeros(2, 2, dtype=torch.int32), torch.zeros(2, dtype=torch.int32))
+
+
+@pytest.mark.parametrize("changes,code,needle", [
+    (dict(indices=1 << 20, topk=64, indices_stride=64, s_q=2), 4, b"s_q"),
+    (dict(indices=1 << 20, topk=0, indices_stride=64), 4, b"topk"),
+    (dict(indices=1 << 20, topk=4096, indices_stride=4096), 4, b"topk"),
+    (dict(indices=1 << 20, topk=64, indices_stride=32), 1, b"indices_stride"),
+    (dict(indices=1 << 20, topk=64, indices_stride=64, kv_format=1, kv_scale=1 << 20), 4, b"16-bit"),
+    (dict(indices=1 << 20, topk=64, indices_stride=64, block_table=None, cache_seqlens=None), 2, b"workspace"),
+])
+def test_decode_rejects_bad_sparse_args(lib, changes, code, needle):
+    a = _valid_args()
+    for k, v in changes.items():
+        setattr(a, k, v)
+    rc = lib.mla_decode_fwd(ctypes.byref(a), None)
+    assert rc == code
+    assert needle in lib.mla_last_error()

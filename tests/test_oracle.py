@@ -327,3 +327,34 @@ def test_append_oracle_skips_unassigned_pages():
     assert skipped == [1, 3]
     assert lens2[1] == lens[1] and lens2[3] == lens[3]
     assert lens2[0] == lens[0] + 2
+
+
+def test_sparse_oracle_equals_paged_through_dense_indices():
+    torch.manual_seed(3)
+    B, H, nb = 3, 16, 12
+    kv = torch.randn(nb, 64, 1, 576)
+    table = torch.randperm(nb).reshape(B, 4).to(torch.int32)
+    lens = torch.tensor([1, 100, 256], dtype=torch.int32)
+    q = torch.randn(B, 1, H, 576)
+    ref_o, ref_l = R.decode_paged(q, kv, table, lens, 0.05, True)
+    idx = R.dense_indices(table, lens, 300)
+    o, l = R.decode_sparse(q, kv, idx, 0.05)
+    assert torch.allclose(o, ref_o, atol=1e-5) and torch.allclose(l, ref_l, atol=1e-5)
+
+
+def test_sparse_oracle_permutation_and_empty():
+    torch.manual_seed(4)
+    kv = torch.randn(4, 64, 1, 576)
+    q = torch.randn(2, 1, 8, 576)
+    idx = torch.tensor([[5, 70, 200, -1, 3], [-1, -1, 999999, -7, -1]], dtype=torch.int32)
+    o, l = R.decode_sparse(q, kv, idx, 0.1)
+    perm = idx[:, torch.tensor([4, 2, 0, 3, 1])]
+    o2, l2 = R.decode_sparse(q, kv, perm, 0.1)
+    assert torch.allclose(o, o2, atol=1e-6) and torch.allclose(l, l2, atol=1e-6)
+    assert torch.all(o[1] == 0) and torch.all(l[1] == float("-inf"))   # no valid key
+    # one key only: out is that key's latent, lse its score
+    one = torch.tensor([[70], [70]], dtype=torch.int32)
+    o3, l3 = R.decode_sparse(q, kv, one, 0.1)
+    k = kv.reshape(-1, 576)[70]
+    assert torch.allclose(o3[:, 0], k[:512].expand(2, 8, 512), atol=1e-6)
+    assert torch.allclose(l3[:, :, 0], (q[:, 0] @ k) * 0.1, atol=1e-5)
