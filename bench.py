@@ -39,6 +39,9 @@ def parse():
     ap.add_argument("--append", action="store_true",
                     help="measure the paged KV-cache append (mla_kv_append) at every config's "
                          "batch and s_q instead of the decode; one JSON line per config")
+    ap.add_argument("--sparse", action="store_true",
+                    help="measure the sparse (top-k = 2048) decode on synthetic index lists; one JSON "
+                         "line per shape")
     ap.add_argument("--kv-fp8", action="store_true",
                     help="measure the decode over the fp8 (e4m3) latent cache at every config (bf16 "
                          "queries); one JSON line per config")
@@ -156,6 +159,52 @@ def measure(cfg_name, steps, warmup, kv_fp8=False):
                 parts=int(sched.shape[0]), n_splits=n_splits)
 
 
+SPARSE_SHAPES = {  # name: (batch, heads, topk, tokens per sequence)
+    "S1": (64, 128, 2048, 8192),   # DeepSeek-V3.2-style top-2048 over 8K contexts, all heads
+    "S2": (128, 16, 2048, 8192),   # the same per TP-8 rank
+}
+
+
+def measure_sparse(name, steps, warmup):
+    """Sparse decode: each sequence owns tokens_per_seq / 64 random pages of the pool and its
+    top-k list is a random choice of distinct tokens among them."""
+    import torch
+    from mlc_decode_amd.api import flash_mla_with_kvcache, get_mla_metadata
+    B, H, topk, per_seq = SPARSE_SHAPES[name]
+    g = torch.Generator().manual_seed(0)
+    pages = per_seq // 64
+    nb = B * pages
+    kv = torch.randn(nb, 64, 1, 576, generator=g).to(torch.bfloat16).cuda()
+    q = torch.randn(B, 1, H, 576, generator=g).to(torch.bfloat16).cuda()
+    table = torch.randperm(nb, generator=g).reshape(B, pages)
+    idx = torch.empty(B, 1, topk, dtype=torch.int32)
+    for b in range(B):
+        t = torch.randperm(per_seq, generator=g)[:topk]
+        idx[b, 0] = (table[b, t // 64] * 64 + t % 64).to(torch.int32)
+    idx = idx.cuda()
+    lens = torch.zeros(B, dtype=torch.int32, device="cuda")
+    sched, splits = get_mla_metadata(lens, H, 1, topk=topk)
+    out = torch.empty(B, 1, H, 512, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(B, H, 1, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def call():
+        flash_mla_with_kvcache(q, kv, None, None, 512, sched, splits, softmax_scale=576 ** -0.5,
+                               out=out, lse=lse, indices=idx)
+
+    settle_clocks(call, stream)
+    ms = time_gpu(call, steps, warmup, stream)
+    nbytes = B * topk * (576 * 2 + 4) + B * H * (576 + 512) * 2 + B * H * 4
+    flops = 2 * B * H * topk * (576 + 512)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"op": "decode_sparse", "shape": name, "batch": B, "heads": H, "topk": topk,
+            "us_call": round(ms * 1e3, 2), "algorithmic_bytes": nbytes, "tbps": round(gbs / 1e3, 3),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "parts": int(sched.shape[0]), "splits": int(splits[-1].item()),
+            "note": "call = main + combine through the Python API; indices random distinct tokens "
+                    "of each sequence's pages"}
+
+
 def cpu_baseline(m, budget_s):
     """The fp32 CPU oracle (the reference's torch decode, restated in oracle/) on a bounded
     sample of the same workload's sequences, scaled to microseconds per full call."""
@@ -243,6 +292,10 @@ def main():
     if args.append:
         for name in ("C1", "C2", "C3", "C4", "C5"):
             print(json.dumps(measure_append(name, args.steps)), flush=True)
+        return
+    if args.sparse:
+        for name in SPARSE_SHAPES:
+            print(json.dumps(measure_sparse(name, args.steps, args.warmup)), flush=True)
         return
     if args.kv_fp8:
         for name in ("C1", "C2", "C3", "C4", "C5"):
