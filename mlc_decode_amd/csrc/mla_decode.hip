@@ -456,7 +456,12 @@ void mla_splitkv_kernel(KParams p) {
   constexpr int kMergePitch = kDV * 4 + 16;  // wave-split merge: fp32 rows of 512, padded
   constexpr int kMergeBytes = WS ? NW * 16 * kMergePitch : 0;
   constexpr int kSmem = kSlots * kSB > kMergeBytes ? kSlots * kSB : kMergeBytes;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSmem];
+  // fp8 with four loading waves: each stage is dequantised once, a row group per wave, into a
+  // bf16 stage buffer, and the bf16 fragment path reads it (kDeq); the one-wave layouts convert
+  // every fragment on its way to the MFMA instead (kInl8).
+  constexpr bool kDeq = KV8 && NL == 4;
+  constexpr bool kInl8 = KV8 && !kDeq;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSmem + (kDeq ? kStageBytes : 0)];
   // wave-split merge words: (row max, row sum) per wave and row
   __shared__ float merge_sh[WS ? NW : 1][2][16];
   // sparse: the pool-token indices of the current segment
@@ -479,6 +484,7 @@ void mla_splitkv_kernel(KParams p) {
   const int row0 = hb * R + (WS ? 0 : wave * 16 * HT);
   // this wave's stage ring, and the first stage / stride of its turn over a segment
   uint8_t LDS_AS* const ring = smem + (WS ? wave * kSB : 0);
+  uint8_t LDS_AS* const deq = smem + kSmem;  // kDeq: the bf16 stage
   const int k0 = WS ? wave : 0;
   constexpr int kStep = WS ? NW : 1;
 
@@ -546,7 +552,7 @@ void mla_splitkv_kernel(KParams p) {
       const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 16 * g;
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
-        if constexpr (KV8) {
+        if constexpr (kInl8) {
           // dims 32kk + 8g (the fp8 fragments' natural order)
           const int d = 32 * kk - 8 * g;  // qn / qr already point 16g past the row start
           qf[ht][kk] = *(const i32x4*)(kk < 16 ? qn + d : qr + (d - kRopeOff));
@@ -668,7 +674,7 @@ void mla_splitkv_kernel(KParams p) {
 
       // ---- O^T += V^T P^T over the 32 tokens of stage kp; DV fragments in flight
       auto v_base = [&](int kp) __attribute__((always_inline)) {
-        const uint8_t LDS_AS* vb = ring + (kp % NSTAGE) * kSB + v_lane;
+        const uint8_t LDS_AS* vb = (kDeq ? deq : ring + (kp % NSTAGE) * kSB) + v_lane;
         asm volatile("" : "+v"(vb));
         return vb;
       };
@@ -807,7 +813,31 @@ void mla_splitkv_kernel(KParams p) {
           if (k + LEAD < nst) issue(k + LEAD);
         }
 
-        const uint8_t LDS_AS* sb = ring + (k % NSTAGE) * kSB;
+        if constexpr (kDeq) {
+          // dequantise this wave's row group of stage k into the bf16 stage (its layout: row r,
+          // 16-byte chunk c of 64-dim segment s in block (r/8)*9 + s, slot 8(r%8) + (c ^ swz));
+          // rows past the sequence end take the last row's scales (their codes are its copies)
+          const uint8_t LDS_AS* f8 = ring + (k % NSTAGE) * kSB;
+          const int r = 8 * wave + (lane >> 3);
+          const int left = L - (st_begin + k) * kStageTok;
+          const int rs = r < left ? r : left - 1;
+          const int c = (lane & 7) ^ stage_swz(r & 15);
+          float sc[4];
+#pragma unroll
+          for (int b4 = 0; b4 < 4; ++b4) sc[b4] = *(const float LDS_AS*)(f8 + kScaleOff8 + b4 * 1024 + 4 * rs);
+#pragma unroll
+          for (int sg = 0; sg < 8; ++sg) {
+            const int c16 = 4 * (sg & 1) + (c >> 1);
+            const i32x2 raw = *(const i32x2 LDS_AS*)(f8 + (4 * wave + (sg >> 1)) * 1024 +
+                                                     16 * (8 * (r & 7) + (c16 ^ swz8(r))) + 8 * (c & 1));
+            *(i32x4 LDS_AS*)(deq + (9 * wave + sg) * 1024 + 16 * lane) = cvt_fp8x8(raw, sc[sg >> 1]);
+          }
+          *(i32x4 LDS_AS*)(deq + (9 * wave + 8) * 1024 + 16 * lane) =
+              *(const i32x4 LDS_AS*)(f8 + kRopeOff8 + wave * 1024 + 16 * (8 * (r & 7) + (c ^ swzr(r))));
+          wait_lgkm0();
+          lds_barrier();
+        }
+        const uint8_t LDS_AS* sb = kDeq ? (const uint8_t LDS_AS*)deq : ring + (k % NSTAGE) * kSB;
         const int st = st_begin + k;
 
         // ---- S^T = K Q^T over 576 dims: two 16-token tiles x HT 16-row tiles.
@@ -826,7 +856,7 @@ void mla_splitkv_kernel(KParams p) {
         float sk[2][4];
         const uint8_t LDS_AS* kbl = sb + kb8;
         const uint8_t LDS_AS* kbr = sb + kr8;
-        if constexpr (KV8) {
+        if constexpr (kInl8) {
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -849,7 +879,7 @@ void mla_splitkv_kernel(KParams p) {
               kk == 16 ? kbr : (const uint8_t LDS_AS*)(uintptr_t)((uint32_t)(uintptr_t)kbr ^ 64u);
           return *(const i32x4 LDS_AS*)(a + 2048 * tt);
         };
-        if constexpr (KV8) {
+        if constexpr (kInl8) {
           // The converted fragments are VALU results read by the (inline-asm) MFMAs, whose
           // hazards the compiler does not see.  Fragment n+1 is converted before MFMA n issues
           // (so an MFMA separates every conversion from its reader), and fragment n-1 is held
@@ -919,7 +949,7 @@ void mla_splitkv_kernel(KParams p) {
         i32x4 vf[DV];
         i32x2 vr[DV];
         if constexpr (MODE != kPassRowMax) {
-          if constexpr (KV8) v8_prefetch(k, vr);
+          if constexpr (kInl8) v8_prefetch(k, vr);
           else v_prefetch(k, vf);
         }
 
@@ -1001,7 +1031,7 @@ void mla_splitkv_kernel(KParams p) {
             for (int r = 0; r < 4; ++r) pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
           l_part[ht] += ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) +
                         ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3]));
-          if constexpr (KV8) {
+          if constexpr (kInl8) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -1012,7 +1042,7 @@ void mla_splitkv_kernel(KParams p) {
           }
         }
 
-        if constexpr (KV8) pv_stage8(k, pvf, vr);
+        if constexpr (kInl8) pv_stage8(k, pvf, vr);
         else pv_stage(k, pb, vf);
         refill_single(k);
         if constexpr (MODE == kPassFirstStageRef && !WS) wait_lgkm0();  // flag store lands before the barrier
