@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--sparse", action="store_true",
                     help="measure the sparse (top-k = 2048) decode on synthetic index lists; one JSON "
                          "line per shape")
+    ap.add_argument("--absorb", action="store_true",
+                    help="time the fused combine + absorbed W_UV projection against combine + bmm")
     ap.add_argument("--kv-fp8", action="store_true",
                     help="measure the decode over the fp8 (e4m3) latent cache at every config (bf16 "
                          "queries); one JSON line per config")
@@ -205,6 +207,62 @@ def measure_sparse(name, steps, warmup):
                     "of each sequence's pages"}
 
 
+def measure_absorb(cfg_name, steps, warmup):
+    """Absorbed value projection v = o . W_UV per head after the decode: the fused kernel
+    (combine merged into the product's prologue, ``mla_combine_absorb``) against the unfused
+    pair (combine kernel, then torch's batched product).  Weights are random N(0, 1/512)."""
+    import ctypes
+
+    import torch
+    from mlc_decode_amd import _lib
+    from mlc_decode_amd._lib import check
+    from mlc_decode_amd.api import get_mla_metadata, make_decode_args, prepare_w_uv
+    from mlc_decode_amd.inputs import CONFIGS, make_inputs
+
+    cfg = CONFIGS[cfg_name]
+    inp = make_inputs(cfg, seed=0).to("cuda:0")
+    B, s_q, H = cfg.batch, cfg.s_q, cfg.heads
+    M = B * s_q
+    g = torch.Generator().manual_seed(1)
+    w_uv = (torch.randn(H, 512, 128, generator=g) * 512 ** -0.5).to(cfg.dtype).cuda()
+    w_t = prepare_w_uv(w_uv)
+    sched, splits = get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=cfg.num_splits or 0)
+    out = torch.empty(B, s_q, H, 512, dtype=cfg.dtype, device="cuda:0")
+    lse = torch.empty(B, H, s_q, dtype=torch.float32, device="cuda:0")
+    v = torch.empty(B, s_q, H, 128, dtype=cfg.dtype, device="cuda:0")
+    lib = _lib.load()
+    args, _, _, keep = make_decode_args(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                        sched, splits, inp.sm_scale, inp.causal, out, lse)
+    ap = ctypes.byref(args)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    check("mla_splitkv_fwd", lib.mla_splitkv_fwd(ap, sp))  # partials and single-split rows in place
+
+    def fused():
+        check("mla_combine_absorb", lib.mla_combine_absorb(ap, w_t.data_ptr(), v.data_ptr(), sp))
+
+    def unfused():
+        check("mla_combine_fwd", lib.mla_combine_fwd(ap, sp))
+        torch.matmul(out.view(M, H, 512).transpose(0, 1), w_uv)
+
+    settle_clocks(fused, stream)
+    ms_fused = time_gpu(fused, steps, warmup, stream)
+    ms_unfused = time_gpu(unfused, steps, warmup, stream)
+    torch.cuda.synchronize()
+    del keep
+    n = (splits[1:] - splits[:-1]).cpu()
+    rows = s_q * H
+    part_bytes = int(sum(rows * (1024 if k == 1 else k * (1024 + 4)) for k in n.tolist()))
+    nbytes = H * 128 * 512 * 2 + part_bytes + M * H * 128 * 2
+    flops = 2 * M * H * 512 * 128
+    gbs = nbytes / (ms_fused * 1e-3) / 1e9
+    return {"op": "combine_absorb", "config": cfg_name, "rows": M, "heads": H,
+            "us_fused": round(ms_fused * 1e3, 2), "us_combine_then_bmm": round(ms_unfused * 1e3, 2),
+            "algorithmic_bytes": nbytes, "tbps": round(gbs / 1e3, 3), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tflops": round(flops / (ms_fused * 1e-3) / 1e12, 1), "splits": int(splits[-1].item()),
+            "note": "bytes = W_UV + split partials (or the single-split row) + v; decode not timed"}
+
+
 def cpu_baseline(m, budget_s):
     """The fp32 CPU oracle (the reference's torch decode, restated in oracle/) on a bounded
     sample of the same workload's sequences, scaled to microseconds per full call."""
@@ -296,6 +354,10 @@ def main():
     if args.sparse:
         for name in SPARSE_SHAPES:
             print(json.dumps(measure_sparse(name, args.steps, args.warmup)), flush=True)
+        return
+    if args.absorb:
+        for name in ("C1", "C2", "C3", "C4", "C5"):
+            print(json.dumps(measure_absorb(name, args.steps, args.warmup)), flush=True)
         return
     if args.kv_fp8:
         for name in ("C1", "C2", "C3", "C4", "C5"):

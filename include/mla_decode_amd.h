@@ -270,6 +270,21 @@ int mla_launch(const void* q, const void* q_pe, const void* kv, const void* k_pe
  * as in mla_decode_args (one tensor or two views).  Returns 0, MLA_ERR_INVALID (bad shape,
  * pointer, alignment or stride; nothing is launched) or MLA_ERR_HIP.
  */
+/*
+ * Absorbed value projection after the split-KV pass (the step that consumes the decode's
+ * output in an MLA layer; no counterpart in the reference): with the same args as the
+ * preceding mla_splitkv_fwd, merge each (sequence, query, head) row's split partials (the
+ * combine) and multiply it by that head's up-projection, without writing the merged latent row:
+ *   v[b, s, h, n] = sum_k o[b, s, h, k] * W_UV[h][k][n],  k < 512, n < 128,
+ * where w_uv_blk holds W_UV k-blocked by 32, w_uv_blk[h][kb][n][kk] = W_UV[h][32 kb + kk][n]
+ * ([H, 16, 128, 32] contiguous in the query dtype, 16-byte aligned: each MFMA k-step of 16
+ * columns is one contiguous KiB), and v is a contiguous [B, s_q, H, 128] array in that dtype.
+ * The merged row is rounded to the query dtype before the product (as mla_combine_fwd would
+ * store it); lse is written as by mla_combine_fwd.  Replaces mla_combine_fwd in that
+ * pipeline; the output projection by W_O that follows is a plain GEMM.
+ */
+int mla_combine_absorb(const mla_decode_args* args, const void* w_uv_blk, void* v, void* stream);
+
 typedef struct mla_kv_append_args {
   int32_t batch;   /* B >= 1 */
   int32_t n_new;   /* new tokens per sequence, 1 .. 64 */

@@ -39,6 +39,7 @@ EXPORTED = (
     "mla_split_plan",
     "mla_launch",
     "mla_kv_append",
+    "mla_combine_absorb",
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -184,6 +185,8 @@ def load() -> ctypes.CDLL:
         lib.mla_launch.restype = ctypes.c_int
         lib.mla_kv_append.argtypes = [ctypes.POINTER(MlaKvAppendArgs), _vp]
         lib.mla_kv_append.restype = ctypes.c_int
+        lib.mla_combine_absorb.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp, _vp, _vp]
+        lib.mla_combine_absorb.restype = ctypes.c_int
         _lib = lib
         return lib
 

@@ -320,6 +320,52 @@ def flash_mla_with_kvcache(q: torch.Tensor, k_cache, block_table: torch.Tensor,
                    softmax_scale, causal, out, lse, indices)
 
 
+def prepare_w_uv(w_uv: torch.Tensor) -> torch.Tensor:
+    """W_UV ``[H, 512, 128]`` (the per-head latent -> value up-projection) in the layout
+    ``mla_combine_absorb`` reads: k-blocked by 32, ``[H, 16, 128, 32]`` contiguous with
+    ``blk[h, kb, n, kk] = w_uv[h, 32 * kb + kk, n]``.  Done once per weight."""
+    if w_uv.dim() != 3 or w_uv.shape[1] != MLA_DIM_V or w_uv.shape[2] != 128:
+        raise ValueError("w_uv must be [H, 512, 128]")
+    H = w_uv.shape[0]
+    return w_uv.reshape(H, MLA_DIM_V // 32, 32, 128).transpose(2, 3).contiguous()
+
+
+def mla_decode_absorbed(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tensor],
+                        cache_seqlens: Optional[torch.Tensor], tile_scheduler_metadata: torch.Tensor,
+                        num_splits: torch.Tensor, w_uv_blk: torch.Tensor, w_o: Optional[torch.Tensor] = None,
+                        softmax_scale: Optional[float] = None, causal: bool = False,
+                        lse: Optional[torch.Tensor] = None, indices: Optional[torch.Tensor] = None):
+    """Decode followed by the absorbed output projection -> ``(y, lse)``.
+
+    The split-KV pass runs as in ``flash_mla_with_kvcache``; its partials are merged straight
+    into the per-head product ``v[b, s, h] = o[b, s, h] . W_UV[h]`` (``mla_combine_absorb``,
+    ``w_uv_blk`` from ``prepare_w_uv``), so the merged latent output is never written.  ``y`` is
+    ``v [B, s_q, H, 128]``, or with ``w_o [H * 128, D]`` the output projection
+    ``v.reshape(B, s_q, H * 128) @ w_o`` (a plain GEMM, done by torch).  No counterpart in the
+    reference; the step that consumes the decode's ``out [B, s_q, H, 512]`` in DeepSeek MLA.
+    """
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** -0.5
+    B, s_q, H, _ = q.shape
+    if (w_uv_blk.shape != (H, MLA_DIM_V // 32, 128, 32) or w_uv_blk.dtype != q.dtype
+            or not w_uv_blk.is_contiguous()):
+        raise ValueError("w_uv_blk must be a contiguous [H, 16, 128, 32] tensor in q's dtype (see prepare_w_uv)")
+    _require_gpu(w_uv_blk, "w_uv_blk")
+    a, out, lse, keep = make_decode_args(q, kv_cache, block_table, cache_seqlens, tile_scheduler_metadata,
+                                         num_splits, softmax_scale, causal, None, lse, indices)
+    v = torch.empty(B, s_q, H, 128, dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    st = _stream_ptr(q.device)
+    check("mla_splitkv_fwd", lib.mla_splitkv_fwd(ctypes.byref(a), st))
+    check("mla_combine_absorb", lib.mla_combine_absorb(ctypes.byref(a), w_uv_blk.data_ptr(), v.data_ptr(), st))
+    del keep
+    if w_o is None:
+        return v, lse
+    if w_o.dim() != 2 or w_o.shape[0] != H * 128 or w_o.dtype != q.dtype:
+        raise ValueError("w_o must be [H * 128, D] in q's dtype")
+    return torch.matmul(v.reshape(B, s_q, H * 128), w_o), lse
+
+
 def mla_decode_with_kvcache(q: torch.Tensor, kv_cache, block_table: torch.Tensor,
                             cache_seqlens: torch.Tensor,
                             num_splits: Union[None, int, Tuple[torch.Tensor, torch.Tensor]] = None,

@@ -1302,8 +1302,7 @@ __device__ __forceinline__ void load8(const float* src, float (&x)[8]) {
   x[4] = c[0]; x[5] = c[1]; x[6] = c[2]; x[7] = c[3];
 }
 template <int DT>
-__device__ __forceinline__ void load8(const uint16_t* src, float (&x)[8]) {
-  const i32x4 v = *(const i32x4*)src;
+__device__ __forceinline__ void cvt8(const i32x4 v, float (&x)[8]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if constexpr (DT == MLA_DTYPE_BF16) {
@@ -1319,10 +1318,67 @@ __device__ __forceinline__ void load8(const uint16_t* src, float (&x)[8]) {
     }
   }
 }
+template <int DT>
+__device__ __forceinline__ void load8(const uint16_t* src, float (&x)[8]) {
+  cvt8<DT>(*(const i32x4*)src, x);
+}
 
-// One wave per (sequence, row); lane l owns output columns 8l .. 8l+7.  Split weights are
-// exp2(lse_k - lse) with lse the log2-sum-exp2 over the row's splits, staged through LDS so
-// every lane reads them; the partial rows are read four splits at a time (independent loads).
+// Merge of one row's split partials by one wave; lane l owns columns 8l .. 8l+7.  Split weights
+// are exp2(lse_k - lse) with lse the log2-sum-exp2 over the row's n splits, staged through the
+// wave's 64-float LDS slot so every lane reads them; the partial rows are read four splits at a
+// time (independent loads).  Returns lse (log2; -inf when no split saw a key, acc then zero).
+// Shared by the combine and the fused absorb prologue, so both merge with the same arithmetic.
+template <int DT, typename PT>
+__device__ __forceinline__ float merge_splits_wave(const PT* __restrict__ ws_o, const float* __restrict__ ws_lse,
+                                                   int base, int n, int rows, int row, int lane, float* w_sh,
+                                                   float (&acc)[8]) {
+  float mx = -INFINITY;
+  for (int k = lane; k < n; k += 64) mx = fmaxf(mx, ws_lse[(int64_t)(base + k) * rows + row]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  float sum = 0.f;
+  if (mx != -INFINITY)
+    for (int k = lane; k < n; k += 64) sum += fast_exp2(ws_lse[(int64_t)(base + k) * rows + row] - mx);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const float lse2 = sum > 0.f ? mx + __log2f(sum) : -INFINITY;
+
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  const PT* src0 = ws_o + ((int64_t)base * rows + row) * kDV + lane * 8;
+  const int64_t split_stride = (int64_t)rows * kDV;
+  for (int k0 = 0; k0 < n; k0 += 64) {
+    const int k = k0 + lane;
+    float w = 0.f;
+    if (k < n && lse2 != -INFINITY) w = fast_exp2(ws_lse[(int64_t)(base + k) * rows + row] - lse2);
+    w_sh[lane] = w;
+    __builtin_amdgcn_wave_barrier();
+    const int kn = n - k0 < 64 ? n - k0 : 64;
+    int kk = 0;
+    for (; kk + 4 <= kn; kk += 4) {
+      float x[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load8<DT>(src0 + (k0 + kk + u) * split_stride, x[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wk = w_sh[kk + u];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += wk * x[u][j];
+      }
+    }
+    for (; kk < kn; ++kk) {
+      float x[8];
+      load8<DT>(src0 + (k0 + kk) * split_stride, x);
+      const float wk = w_sh[kk];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += wk * x[j];
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  return lse2;
+}
+
+// One wave per (sequence, row).
 template <int DT, typename PT>
 __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__ ws_o,
                                                           const float* __restrict__ ws_lse,
@@ -1341,57 +1397,205 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__
   const int base = splits[b];
   const int n = splits[b + 1] - base;
   if (n < 1 || (n == 1 && !copy_single)) return;
-
-  float mx = -INFINITY;
-  for (int k = lane; k < n; k += 64) mx = fmaxf(mx, ws_lse[(int64_t)(base + k) * rows + row]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-  float sum = 0.f;
-  if (mx != -INFINITY)
-    for (int k = lane; k < n; k += 64) sum += fast_exp2(ws_lse[(int64_t)(base + k) * rows + row] - mx);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-  const float lse2 = sum > 0.f ? mx + __log2f(sum) : -INFINITY;
-
   float acc[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  const PT* src0 = ws_o + ((int64_t)base * rows + row) * kDV + lane * 8;
-  const int64_t split_stride = (int64_t)rows * kDV;
-  for (int k0 = 0; k0 < n; k0 += 64) {
-    const int k = k0 + lane;
-    float w = 0.f;
-    if (k < n && lse2 != -INFINITY) w = fast_exp2(ws_lse[(int64_t)(base + k) * rows + row] - lse2);
-    w_sh[wave][lane] = w;
-    __builtin_amdgcn_wave_barrier();
-    const int kn = n - k0 < 64 ? n - k0 : 64;
-    int kk = 0;
-    for (; kk + 4 <= kn; kk += 4) {
-      float x[4][8];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) load8<DT>(src0 + (k0 + kk + u) * split_stride, x[u]);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float wk = w_sh[wave][kk + u];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += wk * x[u][j];
-      }
-    }
-    for (; kk < kn; ++kk) {
-      float x[8];
-      load8<DT>(src0 + (k0 + kk) * split_stride, x);
-      const float wk = w_sh[wave][kk];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += wk * x[j];
-    }
-    __builtin_amdgcn_wave_barrier();
-  }
+  const float lse2 = merge_splits_wave<DT>(ws_o, ws_lse, base, n, rows, row, lane, w_sh[wave], acc);
   const int s = row / heads;
   const int h = row - s * heads;
   uint16_t* dst = out + b * o_sb + s * o_ss + h * o_sh + lane * 8;
   *(i32x4*)dst = i32x4{(int)pack2<DT>(acc[0], acc[1]), (int)pack2<DT>(acc[2], acc[3]),
                        (int)pack2<DT>(acc[4], acc[5]), (int)pack2<DT>(acc[6], acc[7])};
   if (lane == 0 && lse_out != nullptr) lse_out[((int64_t)b * heads + h) * s_q + s] = lse2 * kLn2;
+}
+
+// ---------------------------------------------------------------------------------------
+// absorbed value projection with the combine fused into its prologue
+// ---------------------------------------------------------------------------------------
+// v[m, h, :] = o[m, h, :] . W_UV[h]  (m = b * s_q + s, o the merged latent output, W_UV[h] the
+// head's 512 x kVDim up-projection, given k-blocked: w_blk[h][kb][n][kk] = W_UV[h][32kb + kk][n],
+// so the B operand of one MFMA k-step for 16 columns is one contiguous KiB).  One workgroup of
+// 4 waves per (head, tile of 16 rows); wave w merges rows 4w .. 4w+3 and owns output columns
+// 32w .. 32w+31.  The kernel is a chain of dependent memory round trips, so it is arranged to
+// have few:
+//  1. the rows' split ranges are loaded;
+//  2. the lse of each row's first 64 splits and the partial rows of its first kPF splits are
+//     loaded together (the partials do not depend on the weights); the rows are merged into LDS
+//     as bf16, never written to HBM (a single-split row is read from `out`, where the decode
+//     wrote it).  Each row follows the combine's arithmetic operation for operation
+//     (merge_splits_wave): the same lse (lane-strided max and sum, xor-butterfly), the same
+//     weights, the same fma chain in split order;
+//  3. the wave's W_UV slab (32 columns, 128 registers) is loaded in one round trip and 2 MFMA
+//     tiles form the 16 x kVDim product.
+// At most 168 registers: three workgroups per CU.  (Measured alternatives: loading W_UV before
+// the merge, and 32-row workgroups of 8 waves that preload their 16-column slabs, were no
+// faster; the [h][n][k] layout, 16 half-lines per load, cost 3 us more at 128 heads x 64 rows.)
+constexpr int kVDim = 128;
+constexpr int kAbsRows = 16;
+struct AbsorbParams {
+  const uint16_t* ws_o;  // [slots, rows, 512] partials
+  const float* ws_lse;   // [slots, rows] log2
+  const int32_t* splits;
+  const uint16_t* out;   // single-split rows
+  int64_t o_sb, o_ss, o_sh;
+  const uint16_t* w_blk;  // [H, 16, kVDim, 32]
+  uint16_t* v;           // [M, H, kVDim]
+  float* lse;            // [B, H, s_q] natural log, or null
+  int32_t m_rows, s_q, heads, rows;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams a) {
+  constexpr int RT = kAbsRows;     // rows per workgroup
+  constexpr int kPitch = kDV + 8;  // 16-bit elements; 1040-byte rows keep the A reads conflict-free
+  constexpr int R = RT / 4;        // rows merged by one wave
+  constexpr int NT = 2;            // 16-column MFMA tiles per wave
+  constexpr int KS = kDV / 32;     // MFMA k-steps
+  constexpr int kPF = 4;           // partial rows per row loaded in one round trip
+  __shared__ __attribute__((aligned(16))) uint16_t a_sh[RT * kPitch];
+  __shared__ float w_sh[RT][64];
+  const int h = blockIdx.x;
+  const int m0 = blockIdx.y * RT;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, li = lane & 15;
+
+  // ---- 1. split ranges of the wave's rows
+  const int r0 = wave * R;
+  const int64_t split_stride = (int64_t)a.rows * kDV;
+  int n[R];
+  const uint16_t* src[R];
+  const float* lsep[R];
+  int nmax = 0;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int m = m0 + r0 + i;
+    n[i] = 0;
+    src[i] = a.out;
+    lsep[i] = a.ws_lse;
+    if (m < a.m_rows) {
+      const int b = m / a.s_q, s = m - b * a.s_q;
+      const int row = s * a.heads + h;
+      const int base = a.splits[b];
+      n[i] = a.splits[b + 1] - base;
+      if (n[i] == 1) {
+        src[i] = a.out + b * a.o_sb + s * a.o_ss + h * a.o_sh + lane * 8;
+      } else {
+        src[i] = a.ws_o + ((int64_t)base * a.rows + row) * kDV + lane * 8;
+        lsep[i] = a.ws_lse + (int64_t)base * a.rows + row;
+      }
+    }
+    nmax = n[i] > nmax ? n[i] : nmax;
+  }
+
+  // ---- 2. partial rows of the first kPF splits, and the lse of split `lane`, in one round trip
+  i32x4 x[kPF][R];
+#pragma unroll
+  for (int u = 0; u < kPF; ++u)
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      if (u < n[i]) x[u][i] = *(const i32x4*)(src[i] + u * split_stride);
+  float l0[R], lse2[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) l0[i] = (n[i] > 1 && lane < n[i]) ? lsep[i][(int64_t)lane * a.rows] : 0.f;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    lse2[i] = -INFINITY;
+    if (n[i] > 1) {
+      float mx = -INFINITY;
+      if (lane < n[i]) mx = fmaxf(mx, l0[i]);
+      for (int k = lane + 64; k < n[i]; k += 64) mx = fmaxf(mx, lsep[i][(int64_t)k * a.rows]);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      float sum = 0.f;
+      if (mx != -INFINITY) {
+        if (lane < n[i]) sum += fast_exp2(l0[i] - mx);
+        for (int k = lane + 64; k < n[i]; k += 64) sum += fast_exp2(lsep[i][(int64_t)k * a.rows] - mx);
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+      lse2[i] = sum > 0.f ? mx + __log2f(sum) : -INFINITY;
+      if (lane == 0 && a.lse != nullptr) {
+        const int m = m0 + r0 + i;
+        const int b = m / a.s_q, s = m - b * a.s_q;
+        a.lse[((int64_t)b * a.heads + h) * a.s_q + s] = lse2[i] * kLn2;
+      }
+    }
+  }
+  float acc[R][8];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+  for (int k0 = 0; k0 < nmax; k0 += 64) {
+    const int k = k0 + lane;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      float w = 0.f;
+      if (n[i] == 1) {
+        w = 1.f;  // fma(1, x, 0) = x: the single-split row as the decode wrote it
+      } else if (k < n[i] && lse2[i] != -INFINITY) {
+        w = fast_exp2((k0 == 0 ? l0[i] : lsep[i][(int64_t)k * a.rows]) - lse2[i]);
+      }
+      w_sh[r0 + i][lane] = w;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int kn = nmax - k0 < 64 ? nmax - k0 : 64;
+    for (int kb = 0; kb < kn; kb += kPF) {
+      if (k0 + kb > 0) {
+#pragma unroll
+        for (int u = 0; u < kPF; ++u)
+#pragma unroll
+          for (int i = 0; i < R; ++i)
+            if (k0 + kb + u < n[i]) x[u][i] = *(const i32x4*)(src[i] + (k0 + kb + u) * split_stride);
+      }
+#pragma unroll
+      for (int u = 0; u < kPF; ++u)
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+          if (k0 + kb + u < n[i]) {
+            float xf[8];
+            cvt8<DT>(x[u][i], xf);
+            const float wk = w_sh[r0 + i][kb + u];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] += wk * xf[j];
+          }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    *(i32x4*)&a_sh[(r0 + i) * kPitch + lane * 8] =
+        i32x4{(int)pack2<DT>(acc[i][0], acc[i][1]), (int)pack2<DT>(acc[i][2], acc[i][3]),
+              (int)pack2<DT>(acc[i][4], acc[i][5]), (int)pack2<DT>(acc[i][6], acc[i][7])};
+
+  // ---- 3. this wave's B fragments (8 consecutive k of one column n) in one round trip, then
+  //         the 16 x kVDim product
+  const uint16_t* wb0 = a.w_blk + (int64_t)h * kVDim * kDV + (32 * wave + li) * 32 + 8 * g;
+  i32x4 bf[KS][NT];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) bf[ks][nt] = *(const i32x4*)(wb0 + (ks * kVDim + 16 * nt) * 32);
+  __syncthreads();
+  f32x4 c[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) c[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const i32x4 af = *(const i32x4*)&a_sh[li * kPitch + 32 * ks + 8 * g];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) c[nt] = mfma32<DT>(af, bf[ks][nt], c[nt]);
+  }
+  // lane (g, li) holds rows 4g .. 4g+3 of column li of each tile
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 4 * g + r;
+      if (m < a.m_rows) {
+        const float v = c[nt][r];
+        const uint32_t pk = pack2<DT>(v, v);
+        a.v[((int64_t)m * a.heads + h) * kVDim + 32 * wave + 16 * nt + li] = (uint16_t)(pk & 0xFFFF);
+      }
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1828,6 +2032,37 @@ int mla_combine_fwd(const mla_decode_args* args, void* stream) {
   if (rc != MLA_OK) return rc;
   const mla::KParams kp = make_params(args);
   return launch_combine(kp, (const uint16_t*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
+}
+
+int mla_combine_absorb(const mla_decode_args* args, const void* w_uv_blk, void* v, void* stream) {
+  int64_t need = 0;
+  const int rc = validate(args, &need);
+  if (rc != MLA_OK) return rc;
+  if (!w_uv_blk || !v) return fail(MLA_ERR_INVALID, "w_uv_blk and v must not be NULL");
+  if (!aligned(w_uv_blk, 16)) return fail(MLA_ERR_INVALID, "w_uv_blk must be 16-byte aligned");
+  if (!aligned(v, 4)) return fail(MLA_ERR_INVALID, "v must be 4-byte aligned");
+  const mla::KParams kp = make_params(args);
+  mla::AbsorbParams a{};
+  a.ws_o = kp.ws_o;
+  a.ws_lse = kp.ws_lse;
+  a.splits = kp.splits;
+  a.out = kp.out;
+  a.o_sb = kp.o_sb; a.o_ss = kp.o_ss; a.o_sh = kp.o_sh;
+  a.w_blk = (const uint16_t*)w_uv_blk;
+  a.v = (uint16_t*)v;
+  a.lse = kp.lse;
+  a.m_rows = kp.batch * kp.s_q;
+  a.s_q = kp.s_q;
+  a.heads = kp.heads;
+  a.rows = kp.rows;
+  const dim3 grid(kp.heads, (a.m_rows + mla::kAbsRows - 1) / mla::kAbsRows);
+  if (args->dtype == MLA_DTYPE_BF16)
+    hipLaunchKernelGGL(mla::mla_combine_absorb_kernel<MLA_DTYPE_BF16>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(mla::mla_combine_absorb_kernel<MLA_DTYPE_F16>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("combine-absorb launch failed: ") + hipGetErrorString(e));
+  return MLA_OK;
 }
 
 int mla_merge_partials(const float* part_o, const float* part_lse, const int32_t* num_splits,

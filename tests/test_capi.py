@@ -195,6 +195,22 @@ def test_decode_rejects_bad_fp8_args(lib, changes, code, needle):
     assert needle in lib.mla_last_error()
 
 
+@pytest.mark.parametrize("w,v,code,needle", [
+    (None, 1 << 20, 1, b"NULL"),
+    (1 << 20, None, 1, b"NULL"),
+    ((1 << 20) + 8, 1 << 20, 1, b"w_uv_blk"),
+    (1 << 20, (1 << 20) + 2, 1, b"4-byte"),
+])
+def test_combine_absorb_rejects_bad_args(lib, w, v, code, needle):
+    a = _valid_args()
+    a.workspace_bytes = 1 << 40  # valid decode arguments: the absorb's own checks decide
+    rc = lib.mla_combine_absorb(ctypes.byref(a), w, v, None)
+    assert rc == code
+    assert needle in lib.mla_last_error()
+    a.workspace_bytes = 0          # the decode arguments are validated first
+    assert lib.mla_combine_absorb(ctypes.byref(a), 1 << 20, 1 << 20, None) == 2
+
+
 def test_metadata_rejects_bad_args(lib):
     seq = (ctypes.c_int32 * 2)(5, 6)
     sched = (ctypes.c_int32 * 64)()
@@ -277,3 +293,16 @@ def test_decode_rejects_bad_sparse_args(lib, changes, code, needle):
     rc = lib.mla_decode_fwd(ctypes.byref(a), None)
     assert rc == code
     assert needle in lib.mla_last_error()
+
+
+def test_prepare_w_uv_layout():
+    # blk[h, kb, n, kk] = W_UV[h, 32 kb + kk, n]: the k-blocked layout mla_combine_absorb reads
+    from mlc_decode_amd.api import prepare_w_uv
+    w = torch.arange(3 * 512 * 128, dtype=torch.float32).reshape(3, 512, 128)
+    blk = prepare_w_uv(w)
+    assert blk.shape == (3, 16, 128, 32) and blk.is_contiguous()
+    for h, kb, n, kk in [(0, 0, 0, 0), (1, 3, 77, 5), (2, 15, 127, 31), (2, 7, 0, 31)]:
+        assert blk[h, kb, n, kk] == w[h, 32 * kb + kk, n]
+    assert torch.equal(blk.transpose(2, 3).reshape(3, 512, 128), w)
+    with pytest.raises(ValueError):
+        prepare_w_uv(w[:, :, :64])

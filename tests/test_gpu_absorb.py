@@ -1,0 +1,134 @@
+"""GPU parity of the absorbed value projection with the combine fused into it
+(``mla_combine_absorb``) against a float32 reference of the same product (the decode oracle's
+output times W_UV per head, then W_O)."""
+import sys
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mlc_decode_amd import (flash_mla_with_kvcache, get_mla_metadata, mla_decode_absorbed,
+                            prepare_w_uv)
+from mlc_decode_amd.inputs import make_inputs
+from oracle import mla_ref as R
+
+from test_gpu_parity import small_cfg
+
+pytestmark = pytest.mark.gpu
+
+# v is rounded to bf16 (8 significant bits) and so is the merged row it is computed from (the
+# decode's own output precision); with weights ~ N(0, 1/512) |v| reaches ~4 for one-key rows.
+# Bar: max-abs error <= 2^-7 of the largest |v| (two bf16 roundings of the largest value), and
+# cosine >= 0.9999 against the fp32 product of the fp32 oracle's rows.
+V_RTOL = 2.0 ** -7
+COS_MIN = 0.9999
+
+
+def say(msg):
+    print(f"[gpu-absorb] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def weights(H, dtype, seed, d_model=0):
+    g = torch.Generator().manual_seed(seed)
+    w_uv = (torch.randn(H, 512, 128, generator=g) * 512 ** -0.5).to(dtype)
+    w_o = (torch.randn(H * 128, d_model, generator=g) * (H * 128) ** -0.5).to(dtype) if d_model else None
+    return w_uv, w_o
+
+
+def check_close(got, ref, atol, what):
+    got = got.float().cpu()
+    assert torch.isfinite(got).all(), f"{what}: non-finite"
+    err = (got - ref).abs().max().item()
+    assert err <= atol, f"{what}: max-abs {err}"
+    if ref.abs().max() > 0:
+        cos = F.cosine_similarity(got.flatten().double(), ref.flatten().double(), dim=0).item()
+        assert cos >= COS_MIN, f"{what}: cosine {cos}"
+
+
+@pytest.mark.parametrize("H,s_q", [(16, 1), (64, 1), (128, 1), (128, 2)])
+@pytest.mark.parametrize("forced", [0, 1, 3])
+def test_absorb_matches_reference(gpu, H, s_q, forced):
+    cfg = small_cfg(f"absorb_h{H}", 5, s_q, H, [0, 1, 100, 700, 3000])
+    inp = make_inputs(cfg, seed=H + forced)
+    w_uv, _ = weights(H, torch.bfloat16, H)
+    d = inp.to("cuda")
+    say(f"absorb H={H} s_q={s_q} forced={forced}")
+    sched, splits = get_mla_metadata(d.cache_seqlens, s_q * H, 1, forced_splits=forced)
+    v, lse = mla_decode_absorbed(d.q, d.kv_cache, d.block_table, d.cache_seqlens, sched, splits,
+                                 prepare_w_uv(w_uv.cuda()), softmax_scale=inp.sm_scale, causal=True)
+    torch.cuda.synchronize()
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, inp.sm_scale, True)
+    ref_v = torch.einsum("bshk,hkn->bshn", ref_o, w_uv.float())
+    check_close(v, ref_v, V_RTOL * ref_v.abs().max().item(), f"v H={H} s_q={s_q} forced={forced}")
+    # the fused merge is the combine kernel's (one shared routine): the rows are bit-identical,
+    # so v differs from the fp32 product of the combine's output only by v's own rounding to
+    # bf16 (half an ulp, <= 2^-8 |v|) and fp32 summation order (<= 2^-14 of sum |o_k w_kn|)
+    out, lse2 = flash_mla_with_kvcache(d.q, d.kv_cache, d.block_table, d.cache_seqlens, 512, sched, splits,
+                                       softmax_scale=inp.sm_scale, causal=True)
+    o2 = out.float().cpu()
+    v2 = torch.einsum("bshk,hkn->bshn", o2, w_uv.float())
+    mag = torch.einsum("bshk,hkn->bshn", o2.abs(), w_uv.float().abs())
+    vv = v.float().cpu()
+    bad = (vv - v2).abs() > v2.abs() * 2.0 ** -8 + mag * 2.0 ** -14 + 1e-6
+    assert not bad.any(), f"fused merge differs from combine at {bad.nonzero()[:4].tolist()}"
+    assert torch.equal(lse.cpu(), lse2.cpu()), "fused lse differs from combine"
+
+
+@pytest.mark.parametrize("forced", [0, 1])
+def test_absorb_large_grid(gpu, forced):
+    # 40 sequences x 2 queries: rows in several 16-row tiles, sequences of ragged lengths
+    H, s_q, B = 128, 2, 40
+    lens = [(37 * i * i + 5 * i) % 900 + 1 for i in range(B)]
+    cfg = small_cfg("absorb_big", B, s_q, H, lens)
+    inp = make_inputs(cfg, seed=21 + forced)
+    w_uv, _ = weights(H, torch.bfloat16, 17)
+    d = inp.to("cuda")
+    say(f"absorb large grid forced={forced}")
+    sched, splits = get_mla_metadata(d.cache_seqlens, s_q * H, 1, forced_splits=forced)
+    v, lse = mla_decode_absorbed(d.q, d.kv_cache, d.block_table, d.cache_seqlens, sched, splits,
+                                 prepare_w_uv(w_uv.cuda()), softmax_scale=inp.sm_scale, causal=True)
+    out, lse2 = flash_mla_with_kvcache(d.q, d.kv_cache, d.block_table, d.cache_seqlens, 512, sched, splits,
+                                       softmax_scale=inp.sm_scale, causal=True)
+    torch.cuda.synchronize()
+    ref_o, _ = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, inp.sm_scale, True)
+    ref_v = torch.einsum("bshk,hkn->bshn", ref_o, w_uv.float())
+    check_close(v, ref_v, V_RTOL * ref_v.abs().max().item(), f"v large grid forced={forced}")
+    o2 = out.float().cpu()
+    v2 = torch.einsum("bshk,hkn->bshn", o2, w_uv.float())
+    mag = torch.einsum("bshk,hkn->bshn", o2.abs(), w_uv.float().abs())
+    bad = (v.float().cpu() - v2).abs() > v2.abs() * 2.0 ** -8 + mag * 2.0 ** -14 + 1e-6
+    assert not bad.any(), f"fused merge differs from combine at {bad.nonzero()[:4].tolist()}"
+    assert torch.equal(lse.cpu(), lse2.cpu())
+
+
+def test_absorb_with_output_projection(gpu):
+    H = 128
+    cfg = small_cfg("absorb_wo", 4, 1, H, [64, 500, 1000, 4096])
+    inp = make_inputs(cfg, seed=3)
+    w_uv, w_o = weights(H, torch.bfloat16, 7, d_model=1024)
+    d = inp.to("cuda")
+    say("absorb + W_O")
+    sched, splits = get_mla_metadata(d.cache_seqlens, H, 1)
+    y, lse = mla_decode_absorbed(d.q, d.kv_cache, d.block_table, d.cache_seqlens, sched, splits,
+                                 prepare_w_uv(w_uv.cuda()), w_o.cuda(), softmax_scale=inp.sm_scale, causal=True)
+    torch.cuda.synchronize()
+    ref_o, _ = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, inp.sm_scale, True)
+    ref_y = torch.einsum("bshk,hkn->bshn", ref_o, w_uv.float()).reshape(4, 1, H * 128) @ w_o.float()
+    check_close(y, ref_y, 2 * V_RTOL * ref_y.abs().max().item(), "y = v W_O")
+
+
+def test_absorb_fp16(gpu):
+    H = 64
+    cfg = small_cfg("absorb_f16", 3, 1, H, [33, 2000, 129], dtype=torch.float16)
+    inp = make_inputs(cfg, seed=5)
+    w_uv, _ = weights(H, torch.float16, 5)
+    d = inp.to("cuda")
+    say("absorb fp16")
+    sched, splits = get_mla_metadata(d.cache_seqlens, H, 1, forced_splits=4)
+    v, _ = mla_decode_absorbed(d.q, d.kv_cache, d.block_table, d.cache_seqlens, sched, splits,
+                               prepare_w_uv(w_uv.cuda()), softmax_scale=inp.sm_scale, causal=True)
+    torch.cuda.synchronize()
+    ref_o, _ = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, inp.sm_scale, True)
+    ref_v = torch.einsum("bshk,hkn->bshn", ref_o, w_uv.float())
+    check_close(v, ref_v, V_RTOL * ref_v.abs().max().item(), "v fp16")
