@@ -132,3 +132,54 @@ def test_absorb_fp16(gpu):
     ref_o, _ = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, inp.sm_scale, True)
     ref_v = torch.einsum("bshk,hkn->bshn", ref_o, w_uv.float())
     check_close(v, ref_v, V_RTOL * ref_v.abs().max().item(), "v fp16")
+
+
+def _fused_equals_combine(v, lse, out, lse2, w_uv, what):
+    o2 = out.float().cpu()
+    v2 = torch.einsum("bshk,hkn->bshn", o2, w_uv.float())
+    mag = torch.einsum("bshk,hkn->bshn", o2.abs(), w_uv.float().abs())
+    bad = (v.float().cpu() - v2).abs() > v2.abs() * 2.0 ** -8 + mag * 2.0 ** -14 + 1e-6
+    assert not bad.any(), f"{what}: fused merge differs from combine at {bad.nonzero()[:4].tolist()}"
+    assert torch.equal(lse.cpu(), lse2.cpu()), f"{what}: lse differs"
+
+
+def test_absorb_fp8_cache(gpu):
+    # the projection reads only the split partials: any cache format the decode takes works
+    from mlc_decode_amd import quantize_kv_cache
+    H = 128
+    cfg = small_cfg("absorb_fp8", 4, 1, H, [5, 300, 1000, 2500])
+    inp = make_inputs(cfg, seed=8)
+    w_uv, _ = weights(H, torch.bfloat16, 8)
+    d = inp.to("cuda")
+    cache = quantize_kv_cache(d.kv_cache)
+    say("absorb fp8 cache")
+    sched, splits = get_mla_metadata(d.cache_seqlens, H, 1, forced_splits=3)
+    v, lse = mla_decode_absorbed(d.q, cache, d.block_table, d.cache_seqlens, sched, splits,
+                                 prepare_w_uv(w_uv.cuda()), softmax_scale=inp.sm_scale, causal=True)
+    out, lse2 = flash_mla_with_kvcache(d.q, cache, d.block_table, d.cache_seqlens, 512, sched, splits,
+                                       softmax_scale=inp.sm_scale, causal=True)
+    torch.cuda.synchronize()
+    _fused_equals_combine(v, lse, out, lse2, w_uv, "fp8")
+
+
+def test_absorb_sparse(gpu):
+    H, B, topk, nb = 64, 3, 700, 30
+    g = torch.Generator().manual_seed(12)
+    kv = torch.randn(nb, 64, 1, 576, generator=g).to(torch.bfloat16).cuda()
+    q = torch.randn(B, 1, H, 576, generator=g).to(torch.bfloat16).cuda()
+    idx = torch.randint(0, nb * 64, (B, 1, topk), generator=g, dtype=torch.int32)
+    idx[:, :, ::7] = -1
+    idx = idx.cuda()
+    w_uv, _ = weights(H, torch.bfloat16, 12)
+    lens = torch.zeros(B, dtype=torch.int32, device="cuda")
+    say("absorb sparse")
+    sched, splits = get_mla_metadata(lens, H, 1, topk=topk, forced_splits=2)
+    v, lse = mla_decode_absorbed(q, kv, None, None, sched, splits, prepare_w_uv(w_uv.cuda()),
+                                 softmax_scale=576 ** -0.5, indices=idx)
+    out, lse2 = flash_mla_with_kvcache(q, kv, None, None, 512, sched, splits, softmax_scale=576 ** -0.5,
+                                       indices=idx)
+    torch.cuda.synchronize()
+    _fused_equals_combine(v, lse, out, lse2, w_uv, "sparse")
+    ref_o, _ = R.decode_sparse(q.cpu(), kv.cpu(), idx.cpu(), 576 ** -0.5)
+    ref_v = torch.einsum("bshk,hkn->bshn", ref_o, w_uv.float())
+    check_close(v, ref_v, V_RTOL * ref_v.abs().max().item(), "v sparse")
