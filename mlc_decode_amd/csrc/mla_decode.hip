@@ -1615,6 +1615,7 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
     int forced, int32_t* __restrict__ sched, int32_t* __restrict__ splits) {
   __shared__ int32_t pg_sh[kMetaMaxBatch];
   __shared__ PackState st_sh[kMetaMaxCand][kMetaThreads];
+  __shared__ PackState fin_sh[kMetaMaxCand];
   __shared__ int64_t red_sh[kMetaThreads / 64];
   __shared__ int ok_sh[kMetaMaxCand];
   __shared__ int last_part_sh;
@@ -1642,16 +1643,40 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
   payload_bounds(total, num_parts, f, &lo, &hi);
   const int ncand = min_payload ? (int)(hi - lo) + 1 : 1;  // <= kMetaMaxCand (host-checked)
   const int chunk = (batch + kMetaThreads - 1) / kMetaThreads;
+  const int nchunks = (batch + chunk - 1) / chunk;  // chunks that hold sequences, <= kMetaThreads
   if (t < ncand) {
+    // The serial pass: one sequence after another, the next one's page count read from LDS
+    // while this one is packed (the chain is otherwise one LDS latency per sequence).  While
+    // every quantity fits 31 bits (any real cache: total < 2^30 pages) the step runs in
+    // 32-bit arithmetic (pack_sequence32, the same rule); otherwise in 64-bit.
     const int64_t T = min_payload ? lo + t : hi;
     PackState st{T, 0, 0};
     bool ok = true;
-    for (int c = 0; c < kMetaThreads; ++c) {
-      st_sh[t][c] = st;
-      const int e = min(batch, (c + 1) * chunk);
-      for (int b = c * chunk; ok && b < e; ++b)
-        ok = pack_sequence(b, pg_sh[b], T, f, st, NoEmit{}) && st.part < num_parts;
+    int n_next = pg_sh[0];
+    if (total < (1ll << 30)) {
+      int remain = (int)T, part = 0, cum = 0;
+      for (int c = 0; c < nchunks; ++c) {
+        st_sh[t][c] = PackState{remain, part, cum};
+        const int e = min(batch, (c + 1) * chunk);
+        for (int b = c * chunk; b < e; ++b) {
+          const int n = n_next;
+          n_next = pg_sh[b + 1 < batch ? b + 1 : b];
+          if (ok) ok = pack_sequence32(n, (int)T, f, remain, part, cum) && part < num_parts;
+        }
+      }
+      st = PackState{remain, part, cum};
+    } else {
+      for (int c = 0; c < nchunks; ++c) {
+        st_sh[t][c] = st;
+        const int e = min(batch, (c + 1) * chunk);
+        for (int b = c * chunk; b < e; ++b) {
+          const int n = n_next;
+          n_next = pg_sh[b + 1 < batch ? b + 1 : b];
+          if (ok) ok = pack_sequence(b, n, T, f, st, NoEmit{}) && st.part < num_parts;
+        }
+      }
     }
+    fin_sh[t] = st;  // the state every empty chunk starts (and ends) in
     ok_sh[t] = ok ? 1 : 0;
   }
   __syncthreads();
@@ -1659,7 +1684,7 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
   for (int i = ncand - 1; i >= 0; --i)
     if (ok_sh[i]) best = i;
   const int64_t T = min_payload ? lo + best : hi;
-  PackState st = st_sh[best][t];
+  PackState st = t < nchunks ? st_sh[best][t] : fin_sh[best];
   if (t == 0) {  // part 0 begins at the first page; its end is written by whoever closes it
     sched[0] = 0;
     sched[1] = 0;

@@ -106,6 +106,33 @@ MLA_HD inline bool pack_sequence(int b, int n, int64_t T, int f, PackState& st, 
   return true;
 }
 
+// pack_sequence without the part records, in 32-bit arithmetic, for T + n + f < 2^31 (the
+// device's serial candidate pass, where each step is on the critical path): the same rule and
+// the same results.
+MLA_HD inline bool pack_sequence32(int n, int T, int f, int& remain, int& part, int& cum) {
+  if (remain >= n + f) {
+    remain -= n + f;
+    cum += 1;
+    return true;
+  }
+  const int take0 = remain - f;
+  int page = take0 > 0 ? take0 : 0;
+  int split = take0 > 0 ? 1 : 0;
+  part += 1;
+  int left = n - page;
+  if (T < left + f) {
+    const int c = T - f;
+    if (c < 1) return false;
+    const int k = (int)(((uint32_t)left + (uint32_t)c - 1u) / (uint32_t)c) - 1;
+    part += k;
+    split += k;
+    left -= k * c;
+  }
+  remain = T - left - f;
+  cum += split + 1;
+  return true;
+}
+
 // Sum over sequences of pages + f, and the payload bounds [lo, hi]: no packing fits num_parts
 // parts below lo, and the greedy packing always fits at hi (every closed part consumes at
 // least hi - f of the total).

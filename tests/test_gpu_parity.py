@@ -179,6 +179,8 @@ def test_schedule_device_matches_host(gpu):
         [4096] * 64,
         # more sequences than the metadata kernel's threads: several per replay chunk
         [rng.choice([0, 1, 64, rng.randint(1, 9000)]) for _ in range(700)],
+        [rng.randint(0, 3000) for _ in range(257)],   # two sequences per chunk, 129 chunks
+        [5],
     ]
     for lengths in cases:
         seq = torch.tensor(lengths, dtype=torch.int32, device=gpu)
