@@ -106,31 +106,27 @@ MLA_HD inline bool pack_sequence(int b, int n, int64_t T, int f, PackState& st, 
   return true;
 }
 
-// pack_sequence without the part records, in 32-bit arithmetic, for T + n + f < 2^31 (the
-// device's serial candidate pass, where each step is on the critical path): the same rule and
-// the same results.
+// pack_sequence without the part records, in 32-bit arithmetic and without branches, for
+// T + n + f < 2^31 (the device's serial candidate pass, where each step is on the critical
+// path): the same rule and the same results.  Both outcomes are computed and one is selected;
+// the continuation count k is only computed when the sequence is cut and its rest does not fit
+// a fresh part (then c = T - f >= 1 is required, as in pack_sequence).
 MLA_HD inline bool pack_sequence32(int n, int T, int f, int& remain, int& part, int& cum) {
-  if (remain >= n + f) {
-    remain -= n + f;
-    cum += 1;
-    return true;
-  }
+  const bool fits = remain >= n + f;
   const int take0 = remain - f;
-  int page = take0 > 0 ? take0 : 0;
-  int split = take0 > 0 ? 1 : 0;
-  part += 1;
-  int left = n - page;
-  if (T < left + f) {
-    const int c = T - f;
-    if (c < 1) return false;
-    const int k = (int)(((uint32_t)left + (uint32_t)c - 1u) / (uint32_t)c) - 1;
-    part += k;
-    split += k;
-    left -= k * c;
-  }
-  remain = T - left - f;
-  cum += split + 1;
-  return true;
+  const int page = take0 > 0 ? take0 : 0;
+  const int split0 = take0 > 0 ? 1 : 0;
+  int left = n - page;  // > 0 whenever the sequence does not fit
+  const bool cut = !fits && T < left + f;
+  const int c = T - f;
+  const uint32_t cu = c > 0 ? (uint32_t)c : 1u;
+  const int k = cut ? (int)(((uint32_t)left + cu - 1u) / cu) - 1 : 0;
+  left -= k * c;
+  const bool ok = !cut || c >= 1;
+  remain = fits ? remain - (n + f) : T - left - f;
+  part += fits ? 0 : 1 + k;
+  cum += fits ? 1 : split0 + k + 1;
+  return ok;
 }
 
 // Sum over sequences of pages + f, and the payload bounds [lo, hi]: no packing fits num_parts

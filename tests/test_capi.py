@@ -306,3 +306,47 @@ def test_prepare_w_uv_layout():
     assert torch.equal(blk.transpose(2, 3).reshape(3, 512, 128), w)
     with pytest.raises(ValueError):
         prepare_w_uv(w[:, :, :64])
+
+
+_PACK32_PROG = r"""
+#include <cstdio>
+#include <cstdint>
+#include "mla_sched.h"
+using namespace mla;
+int main() {
+  uint64_t x = 88172645463325252ull;
+  auto rnd = [&](int m) { x ^= x << 13; x ^= x >> 7; x ^= x << 17; return (int)(x % (uint64_t)m); };
+  long bad = 0, steps = 0;
+  for (int trial = 0; trial < 20000; ++trial) {
+    const int f = rnd(8), T = 1 + rnd(trial % 3 == 0 ? 12 : 400);
+    PackState st{T, 0, 0};
+    int remain = T, part = 0, cum = 0;
+    const int B = 1 + rnd(40);
+    for (int b = 0; b < B; ++b) {
+      const int n = rnd(5) == 0 ? 0 : rnd(trial % 2 ? 30 : 3000);
+      const bool ok64 = pack_sequence(b, n, (int64_t)T, f, st, NoEmit{});
+      const bool ok32 = pack_sequence32(n, T, f, remain, part, cum);
+      ++steps;
+      if (ok64 != ok32) { ++bad; break; }
+      if (!ok64) break;
+      if (st.remain != remain || st.part != part || st.cum != cum) { ++bad; break; }
+    }
+  }
+  std::printf("%ld %ld\n", bad, steps);
+  return 0;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++ to build the schedule header")
+def test_pack_sequence32_equals_pack_sequence(tmp_path):
+    # the device's 32-bit branch-free packing step against the reference step, on random
+    # sequences, payloads (including T <= f) and overheads
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = tmp_path / "pack32.cpp"
+    src.write_text(_PACK32_PROG)
+    exe = tmp_path / "pack32"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", os.path.join(repo, "include"),
+                    "-I", os.path.join(repo, "mlc_decode_amd", "csrc"), "-o", str(exe), str(src)], check=True)
+    bad, steps = map(int, subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split())
+    assert steps > 100000 and bad == 0
