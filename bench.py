@@ -1,4 +1,4 @@
-"""MLA decode benchmark on one MI355X (BASELINE metric: B=64, H=128, L=4096 bf16).
+"""MLA decode benchmark on one MI355X (headline metric: µs per call at B=64, H=128, L=4096, bf16).
 
 A step is one decode call over the whole batch with inputs resident in HBM and the tile
 schedule computed beforehand (it is computed once per decode step and shared by every

@@ -1,6 +1,6 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle on identical inputs.
 
-Bar (BASELINE north_star): output max-abs error <= 1e-2 and cosine >= 0.99999 against the
+Bar: output max-abs error <= 1e-2 and cosine >= 0.99999 against the
 fp32 oracle, LSE within 1e-3; rows with no visible key must give out == 0, lse == -inf.
 Full-size benchmark configs are checked on a sample of their sequences (oracle cost) plus
 whole-output properties.
