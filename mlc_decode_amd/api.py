@@ -211,8 +211,6 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tens
     B, s_q, H, _ = q.shape
     if indices is not None:  # sparse: keys named by index, no page table or lengths
         _require_gpu(indices, "indices")
-        if fp8:
-            raise ValueError("the sparse decode reads the 16-bit cache")
         if s_q != 1:
             raise ValueError("the sparse decode takes s_q == 1")
         if indices.dim() == 3:

@@ -220,6 +220,15 @@ __device__ __forceinline__ void dma16_lane(const void* addr, uint32_t lds_addr) 
       : "v"(addr), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
       : "memory", "m0");
 }
+// 4 bytes per lane from a per-lane address, to LDS at lds_addr + 4 * lane (sparse fp8 scales).
+__device__ __forceinline__ void dma4_lane(const void* addr, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dword %0, off nt"
+      :
+      : "v"(addr), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+      : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Workgroup barrier for LDS hand-off only.  Each wave has already waited for its own DMA
@@ -382,6 +391,42 @@ __device__ __forceinline__ void issue_stage8(uint8_t LDS_AS* slot, const uint8_t
   }
 }
 
+// Sparse decode over the fp8 cache: the same stage layout, each token row gathered from its own
+// pool token (idx_stage[r] = page * 64 + row; rows past the list's end re-read its last row, an
+// id outside the pool reads pool token 0, both masked by the caller).  The scales of the stage's
+// 32 tokens for 128-dim block q are 32 separate floats, gathered by one 4-byte load per lane
+// (lanes 32..63 repeat lanes 0..31 into the unused upper part of the block's scale slot).
+// NL = 4: wave w loads row group w and the scales of block w; NL = 1: everything.
+template <int NL>
+__device__ __forceinline__ void issue_stage8_sparse(uint8_t LDS_AS* slot, const uint8_t* lat_pool,
+                                                    const uint16_t* rope_pool, const float* scale_pool,
+                                                    const int32_t LDS_AS* idx_stage, int valid_rows,
+                                                    int64_t lat_sp, int64_t lat_st, int64_t kr_sp,
+                                                    int64_t kr_st, int64_t ks_sp, int64_t ks_sb,
+                                                    int64_t pool_tokens, int wave, int lane) {
+  static_assert(NL == 1 || NL == 4, "stage loads are split over one or four waves");
+  auto token = [&](int r) {
+    const int t = r < valid_rows ? r : valid_rows - 1;
+    int64_t idx = idx_stage[t];
+    return (idx < 0 || idx >= pool_tokens) ? (int64_t)0 : idx;
+  };
+#pragma unroll
+  for (int qi = 0; qi < 4 / NL; ++qi) {
+    const int q = NL == 1 ? qi : wave;  // uniform
+    const int r = 8 * q + (lane >> 3);
+    const int64_t idx = token(r);
+    const int64_t pg = idx >> 6, rw = idx & 63;
+    const uint8_t* lrow = lat_pool + pg * lat_sp + rw * lat_st + (((lane & 7) ^ swz8(r)) << 4);
+    const char* rrow = (const char*)(rope_pool + pg * kr_sp + rw * kr_st) + (((lane & 7) ^ swzr(r)) << 4);
+#pragma unroll
+    for (int sg = 0; sg < 4; ++sg) dma16_lane(lrow + 128 * sg, (uint32_t)(uintptr_t)(slot + (q * 4 + sg) * 1024));
+    dma16_lane(rrow, (uint32_t)(uintptr_t)(slot + kRopeOff8 + q * 1024));
+    const int64_t sidx = token(lane & 31);
+    const float* sc = scale_pool + (sidx >> 6) * ks_sp + q * ks_sb + (sidx & 63);
+    dma4_lane(sc, (uint32_t)(uintptr_t)(slot + kScaleOff8 + q * 1024));
+  }
+}
+
 // Two OCP e4m3 codes (bytes 2*hi, 2*hi+1 of w) to two bf16 values times 2^exponent(scale).
 template <bool HI>
 __device__ __forceinline__ int cvt_fp8x2(int w, float scale) {
@@ -438,7 +483,6 @@ template <int DT, int NW, int HT, int NSTAGE, bool WS, bool KV8, bool SPARSE = f
 __global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW > 0
                                           ? waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW : 1)
 void mla_splitkv_kernel(KParams p) {
-  static_assert(!(SPARSE && KV8), "the sparse path reads the 16-bit cache");
   static_assert(NW == 1 || NW == 4, "one or four waves per workgroup");
   static_assert(!WS || NSTAGE == 1, "wave-split workgroups give each wave a one-stage slot");
   static_assert(!KV8 || DT == MLA_DTYPE_BF16, "the fp8 cache is read with bf16 queries");
@@ -593,7 +637,14 @@ void mla_splitkv_kernel(KParams p) {
 
     auto issue = [&](int k) __attribute__((always_inline)) {
       const int st = st_begin + k;
-      if constexpr (SPARSE) {
+      if constexpr (SPARSE && KV8) {
+        const int left = L - st * kStageTok;
+        issue_stage8_sparse<NL>(ring + (k % NSTAGE) * kSB, (const uint8_t*)p.kv_nope, p.kv_rope, p.kv_scale,
+                                (const int32_t LDS_AS*)idx_sh + k * kStageTok,
+                                left < kStageTok ? left : kStageTok, p.kv_sp, p.kv_st, p.kr_sp, p.kr_st,
+                                p.ks_sp, p.ks_sb, p.pool_tokens, NL == 1 ? 0 : wave, lane);
+        return;
+      } else if constexpr (SPARSE) {
         const int left = L - st * kStageTok;
         issue_stage_sparse<NL>(ring + (k % NSTAGE) * kSB, p.kv_nope, p.kv_rope,
                                (const int32_t LDS_AS*)idx_sh + k * kStageTok,
@@ -1807,6 +1858,14 @@ hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) 
 template <int DT>
 hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blocks, hipStream_t st) {
   if (kp.indices != nullptr) {  // sparse (top-k) decode
+    if constexpr (DT == MLA_DTYPE_BF16) {
+      if (kp.kv_scale != nullptr) {  // over the fp8 latent cache
+        if (v.ws) return launch_main<DT, 4, 1, 1, true, true, true>(kp, head_blocks, st);
+        if (v.nw == 1) return launch_main<DT, 1, 2, 1, false, true, true>(kp, head_blocks, st);
+        if (v.ht == 1) return launch_main<DT, 4, 1, 4, false, true, true>(kp, head_blocks, st);
+        return launch_main<DT, 4, 2, 3, false, true, true>(kp, head_blocks, st);
+      }
+    }
     if (v.ws) return launch_main<DT, 4, 1, 1, true, false, true>(kp, head_blocks, st);
     if (v.nw == 1) return launch_main<DT, 1, 2, 1, false, false, true>(kp, head_blocks, st);
     if (v.ht == 1) return launch_main<DT, 4, 1, 4, false, false, true>(kp, head_blocks, st);
@@ -1867,7 +1926,6 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
     return fail(MLA_ERR_INVALID, "kv_format must be MLA_KV_NATIVE or MLA_KV_FP8_E4M3 (kv_reserved 0)");
   if (a->indices) {
     if (a->s_q != 1) return fail(MLA_ERR_UNSUPPORTED, "the sparse decode takes s_q == 1");
-    if (a->kv_format != MLA_KV_NATIVE) return fail(MLA_ERR_UNSUPPORTED, "the sparse decode reads the 16-bit cache");
     if (a->topk < 1 || a->topk > MLA_SPARSE_MAX_TOPK)
       return fail(MLA_ERR_UNSUPPORTED, "topk must be in [1, MLA_SPARSE_MAX_TOPK]");
     if (a->indices_stride < a->topk) return fail(MLA_ERR_INVALID, "indices_stride must be >= topk");
@@ -1877,7 +1935,7 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
   }
   if (a->kv_format == MLA_KV_FP8_E4M3) {
     if (a->dtype != MLA_DTYPE_BF16) return fail(MLA_ERR_UNSUPPORTED, "the fp8 cache is read with bf16 queries");
-    if (!a->block_table) return fail(MLA_ERR_UNSUPPORTED, "the fp8 cache is paged only");
+    if (!a->block_table && !a->indices) return fail(MLA_ERR_UNSUPPORTED, "the fp8 cache is paged only");
     if (a->kv_stride_page % 16 || a->kv_stride_tok % 16)
       return fail(MLA_ERR_INVALID, "fp8 latent strides must be multiples of 16 bytes");
     if (!a->kv_scale || !aligned(a->kv_scale, 16) || a->kv_scale_stride_page < 0 ||

@@ -283,7 +283,9 @@ def test_kv_append_python_checks():
     (dict(indices=1 << 20, topk=0, indices_stride=64), 4, b"topk"),
     (dict(indices=1 << 20, topk=4096, indices_stride=4096), 4, b"topk"),
     (dict(indices=1 << 20, topk=64, indices_stride=32), 1, b"indices_stride"),
-    (dict(indices=1 << 20, topk=64, indices_stride=64, kv_format=1, kv_scale=1 << 20), 4, b"16-bit"),
+    # over the fp8 cache (no page table needed): valid up to the workspace check
+    (dict(indices=1 << 20, topk=64, indices_stride=64, kv_format=1, kv_scale=1 << 20, block_table=None),
+     2, b"workspace"),
     (dict(indices=1 << 20, topk=64, indices_stride=64, block_table=None, cache_seqlens=None), 2, b"workspace"),
 ])
 def test_decode_rejects_bad_sparse_args(lib, changes, code, needle):

@@ -89,3 +89,26 @@ def test_sparse_with_dense_indices_equals_dense_kernel(gpu):
     assert (sl - dl).abs().max().item() <= 1e-4
     ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, inp.sm_scale)
     assert_parity(so, sl, ref_o, ref_l, "sparse dense-order")
+
+
+@pytest.mark.parametrize("H", [16, 32, 64, 128])
+def test_sparse_fp8_cache(gpu, H):
+    # the top-k decode over the fp8 latent cache: the fp32 oracle of the dequantised pool, and
+    # the sparse kernel on the dequantised (bf16-exact) pool
+    from mlc_decode_amd import Fp8KVCache
+    from oracle import mla_fp8_ref as F8
+    q, kv, idx = sparse_case(3, H, 333, nb=24, seed=H + 1)
+    lat, sc, rope = F8.quantize_pages(kv)
+    deq = F8.dequantize_pages(lat, sc, rope)
+    cache = Fp8KVCache(torch.from_numpy(lat).cuda(), torch.from_numpy(sc).cuda(), rope.cuda())
+    say(f"sparse fp8 H={H}")
+    dummy = torch.zeros(3, dtype=torch.int32, device="cuda")
+    sched, splits = get_mla_metadata(dummy, H, 1, topk=333)
+    out, lse = flash_mla_with_kvcache(q.cuda(), cache, None, None, 512, sched, splits,
+                                      softmax_scale=576 ** -0.5, indices=idx.cuda())
+    torch.cuda.synchronize()
+    ref_o, ref_l = R.decode_sparse(q, deq, idx, 576 ** -0.5)
+    assert_parity(out, lse, ref_o, ref_l, f"sparse fp8 H={H}")
+    o16, l16 = run_sparse(q, deq.to(torch.bfloat16), idx)
+    assert (out.float() - o16.float()).abs().max().item() <= 4e-3
+    assert (lse - l16).abs().max().item() <= 1e-4
