@@ -167,16 +167,18 @@ SPARSE_SHAPES = {  # name: (batch, heads, topk, tokens per sequence)
 }
 
 
-def measure_sparse(name, steps, warmup):
+def measure_sparse(name, steps, warmup, kv_fp8=False):
     """Sparse decode: each sequence owns tokens_per_seq / 64 random pages of the pool and its
     top-k list is a random choice of distinct tokens among them."""
     import torch
-    from mlc_decode_amd.api import flash_mla_with_kvcache, get_mla_metadata
+    from mlc_decode_amd.api import flash_mla_with_kvcache, get_mla_metadata, quantize_kv_cache
     B, H, topk, per_seq = SPARSE_SHAPES[name]
     g = torch.Generator().manual_seed(0)
     pages = per_seq // 64
     nb = B * pages
     kv = torch.randn(nb, 64, 1, 576, generator=g).to(torch.bfloat16).cuda()
+    if kv_fp8:
+        kv = quantize_kv_cache(kv)
     q = torch.randn(B, 1, H, 576, generator=g).to(torch.bfloat16).cuda()
     table = torch.randperm(nb, generator=g).reshape(B, pages)
     idx = torch.empty(B, 1, topk, dtype=torch.int32)
@@ -196,10 +198,11 @@ def measure_sparse(name, steps, warmup):
 
     settle_clocks(call, stream)
     ms = time_gpu(call, steps, warmup, stream)
-    nbytes = B * topk * (576 * 2 + 4) + B * H * (576 + 512) * 2 + B * H * 4
+    token_bytes = FP8_TOKEN_BYTES if kv_fp8 else 576 * 2
+    nbytes = B * topk * (token_bytes + 4) + B * H * (576 + 512) * 2 + B * H * 4
     flops = 2 * B * H * topk * (576 + 512)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"op": "decode_sparse", "shape": name, "batch": B, "heads": H, "topk": topk,
+    return {"op": "decode_sparse_fp8_cache" if kv_fp8 else "decode_sparse", "shape": name, "batch": B, "heads": H, "topk": topk,
             "us_call": round(ms * 1e3, 2), "algorithmic_bytes": nbytes, "tbps": round(gbs / 1e3, 3),
             "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "parts": int(sched.shape[0]), "splits": int(splits[-1].item()),
@@ -353,7 +356,7 @@ def main():
         return
     if args.sparse:
         for name in SPARSE_SHAPES:
-            print(json.dumps(measure_sparse(name, args.steps, args.warmup)), flush=True)
+            print(json.dumps(measure_sparse(name, args.steps, args.warmup, kv_fp8=args.kv_fp8)), flush=True)
         return
     if args.absorb:
         for name in ("C1", "C2", "C3", "C4", "C5"):
