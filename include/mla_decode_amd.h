@@ -83,7 +83,7 @@ extern "C" {
  * lse is a contiguous fp32 [B, H, s_q] array (natural log of the softmax denominator
  * of sm_scale * q.k); rows with no visible key get out = 0 and lse = -inf.
  *
- * kv_format == MLA_KV_FP8_E4M3 (paged only, dtype bf16): kv_nope points to uint8 OCP e4m3
+ * kv_format == MLA_KV_FP8_E4M3 (paged or sparse, dtype bf16): kv_nope points to uint8 OCP e4m3
  * codes (strides in bytes: 16-byte multiples; a token's 512 codes contiguous); kv_rope holds
  * the rope dims in bf16 as above; kv_scale holds fp32 scales, the scale of token row r of
  * page p and 128-dim block j (dims 128j .. 128j+127) at
@@ -132,9 +132,10 @@ typedef struct mla_decode_args {
   const float* kv_scale;
   int64_t kv_scale_stride_page, kv_scale_stride_blk;
 
-  /* Sparse (top-k) decode when indices != NULL (s_q == 1, native cache): the keys of sequence b
-   * are the pool tokens indices[b * indices_stride + j], j < topk (1 .. MLA_SPARSE_MAX_TOPK),
-   * token id = page * 64 + row of the paged cache (kv_nope / kv_rope with the page strides);
+  /* Sparse (top-k) decode when indices != NULL (s_q == 1, either cache format): the keys of
+   * sequence b are the pool tokens indices[b * indices_stride + j], j < topk
+   * (1 .. MLA_SPARSE_MAX_TOPK), token id = page * 64 + row of the paged cache (kv_nope /
+   * kv_rope / kv_scale with the page strides);
    * an index < 0 or >= num_blocks * 64 names no key.  block_table and cache_seqlens are not
    * read; the schedule (tile_sched / num_splits) must be the one mla_get_metadata gives for
    * sequence lengths all equal to topk. */
