@@ -358,3 +358,18 @@ def test_sparse_oracle_permutation_and_empty():
     k = kv.reshape(-1, 576)[70]
     assert torch.allclose(o3[:, 0], k[:512].expand(2, 8, 512), atol=1e-6)
     assert torch.allclose(l3[:, :, 0], (q[:, 0] @ k) * 0.1, atol=1e-5)
+
+
+def test_check_cli_reference_equals_oracle():
+    # the check CLI's float32 reference (python -m mlc_decode_amd.check) computes the same
+    # decode as the oracle, including grouped KV heads
+    from mlc_decode_amd.check import torch_ref
+    g = torch.Generator().manual_seed(4)
+    for b, h, hk, ctx in ((1, 16, 1, 33), (2, 8, 2, 100)):
+        q = torch.randn(b, h, 512, generator=g) * 0.1
+        q_pe = torch.randn(b, h, 64, generator=g) * 0.1
+        kv = torch.randn(b, ctx, hk, 512, generator=g) * 0.1
+        k_pe = torch.randn(b, ctx, hk, 64, generator=g) * 0.1
+        got = torch_ref(q, q_pe, kv, k_pe, b, h, hk, ctx, 512, 64)
+        want = R.decode_contiguous(q, q_pe, kv, k_pe)
+        assert torch.allclose(got, want, atol=1e-6, rtol=1e-5)
