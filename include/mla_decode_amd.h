@@ -196,8 +196,9 @@ int mla_get_metadata_host(const int32_t* cache_seqlens, int32_t batch, int32_t n
 /*
  * Workspace bytes mla_decode_fwd needs for this problem and part count: the per-split
  * log2-domain lse [slots, rows] fp32 (padded to 256 bytes), then the per-split
- * softmax-normalised partial outputs [slots, rows, 512] in the input dtype (16-bit, as the
- * reference's output_partial, mla_decode.py:73-74), with slots = batch + num_parts.
+ * softmax-normalised partial outputs [slots, rows, 512] fp32, with slots = batch + num_parts.
+ * (The reference's output_partial is in the input dtype, mla_decode.py:73-74; fp32 keeps
+ * split outputs to one rounding, which bf16 needs to stay within 1e-2 for |out| in [2, 4).)
  */
 int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t num_parts);
 
@@ -244,18 +245,20 @@ int mla_split_plan(int32_t seqlen_kv, int32_t num_split, int32_t block_n, int32_
                    int32_t* ns_out, int32_t* blocks_per_split_out, int32_t* extra_out);
 
 /*
- * Flat-argument launch for the reference's contiguous layout, mirroring
- * handmade/mla_handmade.py:34-52 (mla_launch(Q, Qpe, KV, Kpe, glse, partial, out, ns)):
- *   Q [B,H,512], Qpe [B,H,64], KV [B,L,1,512], Kpe [B,L,1,64], out [B,H,512] (dtype),
- *   cache_seqlens [B] int32 (device), tile_sched / num_splits from mla_get_metadata,
- *   workspace of mla_workspace_bytes(B, 1, H, num_parts) bytes.  sm_scale = 576^-0.5.
- * The reference's glse / partial buffers are the workspace here.
+ * The reference's handmade entry point with its exact signature and calling convention
+ * (handmade/mla_handmade.py:34-52; its caller binds argtypes [c_void_p] * 7 + [c_int] and
+ * restype None, :97-107).  Fixed shape, as the reference's generated kernel: batch 1, 16 query
+ * heads, one latent KV head, 8192 cached tokens, fp16, sm_scale = 576^-0.5, contiguous layout
+ *   Q [1, 16, 512], Qpe [1, 16, 64], KV [1, 8192, 1, 512], Kpe [1, 8192, 1, 64], out [1, 16, 512].
+ * glse (fp16 [1, 16, ns + 64]) and partial (fp16 [1, 16, ns, 576]) are the caller's scratch,
+ * as in the reference: glse holds the length and the tile schedule, partial the per-split
+ * lse and 16-bit partial rows (the reference's own partial format).  ns = the number of KV
+ * splits, 1 .. 128 (forced: the 128 pages cut into ns near-equal ranges).  Runs on the null
+ * stream (stream 0) and returns nothing, as the reference; an invalid argument launches
+ * nothing and a failure is reported through mla_last_error() (the reference checks nothing).
  */
-int mla_launch(const void* q, const void* q_pe, const void* kv, const void* k_pe, void* out,
-               int32_t batch, int32_t heads, int32_t kv_ctx, int32_t dtype,
-               const int32_t* cache_seqlens, const int32_t* tile_sched, int32_t num_parts,
-               const int32_t* num_splits, void* workspace, int64_t workspace_bytes,
-               void* stream);
+void mla_launch(const void* Q, const void* Qpe, const void* KV, const void* Kpe, void* glse,
+                void* partial, void* out, int ns);
 
 /*
  * Paged KV-cache append: the step before decode that writes the new tokens' latent + rope rows

@@ -180,9 +180,9 @@ def load() -> ctypes.CDLL:
         lib.mla_merge_partials.restype = ctypes.c_int
         lib.mla_split_plan.argtypes = [_i32, _i32, _i32, _i32, _pi32, _pi32, _pi32]
         lib.mla_split_plan.restype = ctypes.c_int
-        lib.mla_launch.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp,
-                                   _i32, _vp, _vp, _i64, _vp]
-        lib.mla_launch.restype = ctypes.c_int
+        # the reference's binding of its handmade entry point (handmade/mla_handmade.py:97-107)
+        lib.mla_launch.argtypes = [_vp] * 7 + [ctypes.c_int]
+        lib.mla_launch.restype = None
         lib.mla_kv_append.argtypes = [ctypes.POINTER(MlaKvAppendArgs), _vp]
         lib.mla_kv_append.restype = ctypes.c_int
         lib.mla_combine_absorb.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp, _vp, _vp]

@@ -81,7 +81,8 @@ struct KParams {
   int64_t o_sb, o_ss, o_sh;
   float* lse;
   float* ws_lse;    // [slots, rows] log2-domain lse of each split
-  uint16_t* ws_o;   // [slots, rows, 512] softmax-normalised partial outputs, input dtype
+  float* ws_o;      // [slots, rows, 512] softmax-normalised partial outputs, fp32
+  int32_t part16;   // nonzero: ws_o holds the partials in the input dtype instead (mla_launch)
   // fp8 latent cache only: kv_nope holds e4m3 codes (strides in bytes) and kv_scale the fp32
   // power-of-two scales, [page][128-dim block][token] with strides ks_sp, ks_sb (floats)
   const float* kv_scale;
@@ -164,6 +165,23 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
   else
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// acc + the sum of the eight 16-bit values packed in w (one v_dot2c_f32_{bf16,f16} per pair,
+// fp32 accumulation).  The softmax row sums are taken over the P values as rounded for the PV
+// product, so the weights applied to V sum to exactly the denominator.
+template <int DT>
+__device__ __forceinline__ float packed_sum(const i32x4 w, float acc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t x = (uint32_t)w[j];  // element copied out before the bit cast
+    if constexpr (DT == MLA_DTYPE_BF16)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), bf16x2{(__bf16)1.f, (__bf16)1.f}, acc,
+                                            false);
+    else
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), f16x2{(_Float16)1, (_Float16)1}, acc, false);
+  }
+  return acc;
 }
 
 // max of three floats in one v_max3_f32 (fmaxf would first canonicalise each operand for
@@ -506,8 +524,8 @@ void mla_splitkv_kernel(KParams p) {
   constexpr bool kDeq = KV8 && NL == 4;
   constexpr bool kInl8 = KV8 && !kDeq;
   __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSmem + (kDeq ? kStageBytes : 0)];
-  // wave-split merge words: (row max, row sum) per wave and row
-  __shared__ float merge_sh[WS ? NW : 1][2][16];
+  // wave-split merge words: (row max, row sum of rounded P, row sum of fp32 P) per wave and row
+  __shared__ float merge_sh[WS ? NW : 1][3][16];
   // sparse: the pool-token indices of the current segment
   __shared__ int32_t idx_sh[SPARSE ? kSparseMaxTopk : 1];
   // "score above reference" words, one per stage modulo 4.  A wave whose stage-k scores exceed
@@ -620,7 +638,9 @@ void mla_splitkv_kernel(KParams p) {
     }
 
     f32x4 o[kDimTiles][HT];
-    float m_ref[HT], l_part[HT];
+    // row sums: l_part of P as rounded for the PV product (normalises the output), l_exact of
+    // the fp32 P (gives the lse)
+    float m_ref[HT], l_part[HT], l_exact[HT];
     int pbase = 0, bt_lane = 0;
 
     auto load_page_ids = [&](int first) __attribute__((always_inline)) {
@@ -693,7 +713,7 @@ void mla_splitkv_kernel(KParams p) {
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) o[dt][ht] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht) l_part[ht] = 0.f;
+        for (int ht = 0; ht < HT; ++ht) l_part[ht] = l_exact[ht] = 0.f;
       }
       if constexpr (MODE != kPassFixedRef) {
 #pragma unroll
@@ -1080,16 +1100,24 @@ void mla_splitkv_kernel(KParams p) {
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
-          l_part[ht] += ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) +
-                        ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3]));
+          // P rounded to the 16-bit type as the PV product takes it; the row sum counts those
+          // rounded values (a sum of the unrounded ones would leave the weights on V summing
+          // to 1 + O(2^-9): with V far from zero on average that bias does not cancel)
+          const i32x4 pr = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
+                                 (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
+          l_part[ht] = packed_sum<DT>(pr, l_part[ht]);
+          l_exact[ht] += ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) +
+                         ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3]));
           if constexpr (kInl8) {
+            // the V scales are powers of two: P * scale rounds to exactly this P times the scale
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) pvf[ht][4 * tt + r] = pv[tt][r];
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t x = (uint32_t)pr[j];
+              pvf[ht][2 * j] = __uint_as_float(x << 16);
+              pvf[ht][2 * j + 1] = __uint_as_float(x & 0xffff0000u);
+            }
           } else {
-            pb[ht] = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
-                           (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
+            pb[ht] = pr;
           }
         }
 
@@ -1135,7 +1163,8 @@ void mla_splitkv_kernel(KParams p) {
       // ---- wave-split merge.  Wave w holds (m_w, l_w, O_w) over its stages (m_w = -inf and
       // l_w = 0 for a wave that had none); the segment's result is
       //   O = sum_w 2^(m_w - m) O_w / lsum,  lsum = sum_w 2^(m_w - m) l_w,  m = max_w m_w,
-      // and lse = m + log2(lsum) (log2 units, as every split's lse).  Each wave scales its O_w
+      // and lse = m + log2(xsum) with xsum the same sum over the waves' fp32 row sums (log2
+      // units, as every split's lse).  Each wave scales its O_w
       // into LDS (fp32 rows of 512 with a 16-byte pad: conflict-free 16-byte stores), then
       // wave w sums and stores dims 128w .. 128w + 127 of all 16 rows.  The slots are free:
       // every wave waited for its own stage loads before the first barrier.
@@ -1144,21 +1173,24 @@ void mla_splitkv_kernel(KParams p) {
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) {
         const float l_w = wave_sum_g(l_part[ht]);
+        const float x_w = wave_sum_g(l_exact[ht]);
         if (g == 0) {
           merge_sh[wave][0][li] = m_ref[ht];
           merge_sh[wave][1][li] = l_w;
+          merge_sh[wave][2][li] = x_w;
         }
         wait_lgkm0();
         lds_barrier();
         float m = -INFINITY;
 #pragma unroll
         for (int v = 0; v < NW; ++v) m = fmaxf(m, merge_sh[v][0][li]);
-        float lsum = 0.f, c = 0.f;
+        float lsum = 0.f, xsum = 0.f, c = 0.f;
 #pragma unroll
         for (int v = 0; v < NW; ++v) {
           const float mv = merge_sh[v][0][li];
           const float sv = mv == -INFINITY ? 0.f : fast_exp2(mv - m);
           lsum += sv * merge_sh[v][1][li];
+          xsum += sv * merge_sh[v][2][li];
           if (v == wave) c = sv;  // uniform
         }
         c *= lsum > 0.f ? 1.f / lsum : 0.f;
@@ -1186,24 +1218,26 @@ void mla_splitkv_kernel(KParams p) {
           }
           int row = row0 + 16 * ht + r;
           row = row < p.rows ? row : p.rows - 1;
-          const i32x2 lo = i32x2{(int)pack2<DT>(a0[0], a0[1]), (int)pack2<DT>(a0[2], a0[3])};
-          const i32x2 hi = i32x2{(int)pack2<DT>(a1[0], a1[1]), (int)pack2<DT>(a1[2], a1[3])};
-          uint16_t* d;
-          if (single) {  // uniform
+          if (single) {  // uniform: the final output, rounded once to the input dtype
             const int s = row / p.heads;
             const int h = row - s * p.heads;
-            d = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh);
-          } else {
-            d = p.ws_o + (slot * p.rows + row) * kDV;
+            uint16_t* d = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 128 * wave + 4 * cc;
+            *(i32x2*)d = i32x2{(int)pack2<DT>(a0[0], a0[1]), (int)pack2<DT>(a0[2], a0[3])};
+            *(i32x2*)(d + 64) = i32x2{(int)pack2<DT>(a1[0], a1[1]), (int)pack2<DT>(a1[2], a1[3])};
+          } else if (p.part16) {  // uniform: 16-bit partials (the reference's own format)
+            uint16_t* d = (uint16_t*)p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * cc;
+            *(i32x2*)d = i32x2{(int)pack2<DT>(a0[0], a0[1]), (int)pack2<DT>(a0[2], a0[3])};
+            *(i32x2*)(d + 64) = i32x2{(int)pack2<DT>(a1[0], a1[1]), (int)pack2<DT>(a1[2], a1[3])};
+          } else {  // the split's fp32 partial (rounded only once the splits are merged)
+            float* d = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * cc;
+            *(f32x4*)d = a0;
+            *(f32x4*)(d + 64) = a1;
           }
-          d += 128 * wave + 4 * cc;
-          *(i32x2*)d = lo;
-          *(i32x2*)(d + 64) = hi;
         }
         if (wave == 0) {  // uniform: the four lane groups of a row store the same lse
           int row = row0 + 16 * ht + li;
           row = row < p.rows ? row : p.rows - 1;
-          const float lse2 = lsum > 0.f ? m + __log2f(lsum) : -INFINITY;
+          const float lse2 = xsum > 0.f ? m + __log2f(xsum) : -INFINITY;
           const int s = row / p.heads;
           const int h = row - s * p.heads;
           if (single) {
@@ -1219,23 +1253,42 @@ void mla_splitkv_kernel(KParams p) {
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
       const float l = wave_sum_g(l_part[ht]);
+      const float lx = wave_sum_g(l_exact[ht]);
       int row = row0 + 16 * ht + li;
       row = row < p.rows ? row : p.rows - 1;
       const float inv = l > 0.f ? 1.f / l : 0.f;
-      const float lse2 = l > 0.f ? m_ref[ht] + __log2f(l) : -INFINITY;
+      const float lse2 = lx > 0.f ? m_ref[ht] + __log2f(lx) : -INFINITY;
       const int s = row / p.heads;
       const int h = row - s * p.heads;
-      // A single-split sequence writes its output directly; otherwise the split's partial goes
-      // to the workspace in the input dtype (the split partials of the reference's kernel,
-      // mla_decode.py:73-74,192, are in the input dtype too).
+      // A single-split sequence writes its output directly (rounded once to the input dtype);
+      // otherwise the split's partial goes to the workspace in fp32, so the output is still
+      // rounded only once, after the merge.  (The reference's split kernel rounds its partials
+      // to the input dtype, mla_decode.py:73-74,192; for bf16 a second rounding can move an
+      // output in [2, 4) by up to 2^-7, past the 1e-2 parity bar.)
       const int64_t slot = slot0 + split;
-      uint16_t* dst = single ? p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 4 * g
-                             : p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
+      if (single) {  // uniform
+        uint16_t* dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 4 * g;
 #pragma unroll
-      for (int dt = 0; dt < kDimTiles; ++dt) {  // one tile at a time (register pressure)
-        const f32x4 v = o[dt][ht] * inv;
-        *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
-        __builtin_amdgcn_sched_barrier(0);
+        for (int dt = 0; dt < kDimTiles; ++dt) {  // one tile at a time (register pressure)
+          const f32x4 v = o[dt][ht] * inv;
+          *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else if (p.part16) {  // uniform: 16-bit partials (the reference's own format)
+        uint16_t* dst = (uint16_t*)p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          const f32x4 v = o[dt][ht] * inv;
+          *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        float* dst = p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < kDimTiles; ++dt) {
+          *(f32x4*)(dst + 16 * dt) = o[dt][ht] * inv;
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
       if (single) {
         if (p.lse != nullptr) p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
@@ -1343,8 +1396,8 @@ __global__ __launch_bounds__(256) void mla_kv_append_kernel(AppendParams a) {
 // ---------------------------------------------------------------------------------------
 // combine: LSE-weighted merge of the splits of each (sequence, row)
 // ---------------------------------------------------------------------------------------
-// Eight consecutive partial values of one row, widened to fp32: from the fp32 partials of
-// mla_merge_partials or from the 16-bit (input dtype) partials of the decode workspace.
+// Eight consecutive partial values of one row, widened to fp32: the fp32 rows of the decode
+// workspace and of mla_merge_partials, or the 16-bit rows of mla_launch.
 template <int DT>
 __device__ __forceinline__ void load8(const float* src, float (&x)[8]) {
   const f32x4 a = *(const f32x4*)src;
@@ -1482,7 +1535,7 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__
 constexpr int kVDim = 128;
 constexpr int kAbsRows = 16;
 struct AbsorbParams {
-  const uint16_t* ws_o;  // [slots, rows, 512] partials
+  const float* ws_o;     // [slots, rows, 512] fp32 partials
   const float* ws_lse;   // [slots, rows] log2
   const int32_t* splits;
   const uint16_t* out;   // single-split rows
@@ -1500,7 +1553,7 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
   constexpr int R = RT / 4;        // rows merged by one wave
   constexpr int NT = 2;            // 16-column MFMA tiles per wave
   constexpr int KS = kDV / 32;     // MFMA k-steps
-  constexpr int kPF = 4;           // partial rows per row loaded in one round trip
+  constexpr int kPF = 2;           // partial rows (fp32) per row loaded in one round trip
   __shared__ __attribute__((aligned(16))) uint16_t a_sh[RT * kPitch];
   __shared__ float w_sh[RT][64];
   const int h = blockIdx.x;
@@ -1512,14 +1565,16 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
   const int r0 = wave * R;
   const int64_t split_stride = (int64_t)a.rows * kDV;
   int n[R];
-  const uint16_t* src[R];
+  const uint16_t* src1[R];  // single-split rows: the decode's output (input dtype)
+  const float* src[R];      // split rows: fp32 partials
   const float* lsep[R];
   int nmax = 0;
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int m = m0 + r0 + i;
     n[i] = 0;
-    src[i] = a.out;
+    src1[i] = a.out;
+    src[i] = a.ws_o;
     lsep[i] = a.ws_lse;
     if (m < a.m_rows) {
       const int b = m / a.s_q, s = m - b * a.s_q;
@@ -1527,7 +1582,7 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
       const int base = a.splits[b];
       n[i] = a.splits[b + 1] - base;
       if (n[i] == 1) {
-        src[i] = a.out + b * a.o_sb + s * a.o_ss + h * a.o_sh + lane * 8;
+        src1[i] = a.out + b * a.o_sb + s * a.o_ss + h * a.o_sh + lane * 8;
       } else {
         src[i] = a.ws_o + ((int64_t)base * a.rows + row) * kDV + lane * 8;
         lsep[i] = a.ws_lse + (int64_t)base * a.rows + row;
@@ -1535,14 +1590,20 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
     }
     nmax = n[i] > nmax ? n[i] : nmax;
   }
+  // the eight values of split u of row i owned by this lane, widened to fp32 (branches are
+  // wave-uniform: all lanes work on the same row)
+  auto load_row = [&](int u, int i, float (&xv)[8]) __attribute__((always_inline)) {
+    if (n[i] == 1) cvt8<DT>(*(const i32x4*)src1[i], xv);
+    else load8<DT>(src[i] + u * split_stride, xv);
+  };
 
   // ---- 2. partial rows of the first kPF splits, and the lse of split `lane`, in one round trip
-  i32x4 x[kPF][R];
+  float x[kPF][R][8];
 #pragma unroll
   for (int u = 0; u < kPF; ++u)
 #pragma unroll
     for (int i = 0; i < R; ++i)
-      if (u < n[i]) x[u][i] = *(const i32x4*)(src[i] + u * split_stride);
+      if (u < n[i]) load_row(u, i, x[u][i]);
   float l0[R], lse2[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) l0[i] = (n[i] > 1 && lane < n[i]) ? lsep[i][(int64_t)lane * a.rows] : 0.f;
@@ -1595,18 +1656,16 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
         for (int u = 0; u < kPF; ++u)
 #pragma unroll
           for (int i = 0; i < R; ++i)
-            if (k0 + kb + u < n[i]) x[u][i] = *(const i32x4*)(src[i] + (k0 + kb + u) * split_stride);
+            if (k0 + kb + u < n[i]) load_row(k0 + kb + u, i, x[u][i]);
       }
 #pragma unroll
       for (int u = 0; u < kPF; ++u)
 #pragma unroll
         for (int i = 0; i < R; ++i)
           if (k0 + kb + u < n[i]) {
-            float xf[8];
-            cvt8<DT>(x[u][i], xf);
             const float wk = w_sh[r0 + i][kb + u];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[i][j] += wk * xf[j];
+            for (int j = 0; j < 8; ++j) acc[i][j] += wk * x[u][i][j];
           }
     }
     __builtin_amdgcn_wave_barrier();
@@ -1775,6 +1834,18 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
       rec[6] = 0;
       rec[7] = 0;
     }
+  }
+}
+
+// mla_launch's schedule: the reference's frozen shape (one sequence of kHandCtx tokens) cut
+// into ns forced splits, written by one thread into the caller's scratch.
+constexpr int kHandCtx = 8192;
+constexpr int kHandHeads = 16;
+__global__ __launch_bounds__(64) void mla_launch_sched_kernel(int32_t* seqlens, int32_t* sched,
+                                                              int32_t* splits, int ns) {
+  if (threadIdx.x == 0) {
+    seqlens[0] = kHandCtx;
+    schedule_forced(seqlens, 1, ns, sched, splits);
   }
 }
 
@@ -1977,7 +2048,7 @@ mla::KParams make_params(const mla_decode_args* a) {
   const int64_t rows = (int64_t)a->s_q * a->heads_q;
   const int64_t slots = (int64_t)a->batch + a->num_parts;
   k.ws_lse = (float*)a->workspace;
-  k.ws_o = (uint16_t*)((char*)a->workspace + ws_lse_bytes(slots, rows));
+  k.ws_o = (float*)((char*)a->workspace + ws_lse_bytes(slots, rows));
   k.batch = a->batch;
   k.s_q = a->s_q;
   k.heads = a->heads_q;
@@ -1988,8 +2059,8 @@ mla::KParams make_params(const mla_decode_args* a) {
   return k;
 }
 
-// Partials are the 16-bit workspace rows of the decode path (PT = uint16_t) or the caller's
-// fp32 rows of mla_merge_partials (PT = float).
+// Partials are fp32 rows (the decode workspace, the caller's rows of mla_merge_partials) or
+// the 16-bit rows of mla_launch (PT = uint16_t).
 template <typename PT>
 int launch_combine(const mla::KParams& k, const PT* part_o, int dtype, int copy_single, hipStream_t st) {
   dim3 grid(k.batch, (k.rows + 3) / 4);
@@ -2084,14 +2155,14 @@ int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t
   if (batch < 1 || s_q < 1 || heads_q < 1 || num_parts < 1) return 0;
   const int64_t rows = (int64_t)s_q * heads_q;
   const int64_t slots = (int64_t)batch + num_parts;
-  return ws_lse_bytes(slots, rows) + slots * rows * mla::kDV * 2;
+  return ws_lse_bytes(slots, rows) + slots * rows * mla::kDV * 4;
 }
 
 int mla_decode_fwd(const mla_decode_args* args, void* stream) {
   const int rc = mla_splitkv_fwd(args, stream);
   if (rc != MLA_OK) return rc;
   const mla::KParams kp = make_params(args);
-  return launch_combine(kp, (const uint16_t*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
+  return launch_combine(kp, (const float*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
 }
 
 int mla_splitkv_fwd(const mla_decode_args* args, void* stream) {
@@ -2114,7 +2185,7 @@ int mla_combine_fwd(const mla_decode_args* args, void* stream) {
   const int rc = validate(args, &need);
   if (rc != MLA_OK) return rc;
   const mla::KParams kp = make_params(args);
-  return launch_combine(kp, (const uint16_t*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
+  return launch_combine(kp, (const float*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
 }
 
 int mla_combine_absorb(const mla_decode_args* args, const void* w_uv_blk, void* v, void* stream) {
@@ -2194,47 +2265,69 @@ int mla_split_plan(int32_t seqlen_kv, int32_t num_split, int32_t block_n, int32_
   return MLA_OK;
 }
 
-int mla_launch(const void* q, const void* q_pe, const void* kv, const void* k_pe, void* out,
-               int32_t batch, int32_t heads, int32_t kv_ctx, int32_t dtype,
-               const int32_t* cache_seqlens, const int32_t* tile_sched, int32_t num_parts,
-               const int32_t* num_splits, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (kv_ctx < 1) return fail(MLA_ERR_INVALID, "kv_ctx must be >= 1");
-  mla_decode_args a{};
-  a.batch = batch;
-  a.s_q = 1;
-  a.heads_q = heads;
-  a.heads_k = 1;
-  a.dtype = dtype;
-  a.causal = 0;
-  a.sm_scale = 1.0f / sqrtf((float)MLA_DIM_QK);
-  a.num_blocks = 1;
-  a.q_nope = q;
-  a.q_rope = q_pe;
-  a.q_stride_b = (int64_t)heads * 512;
-  a.q_stride_s = 0;
-  a.q_stride_h = 512;
-  a.q_rope_stride_b = (int64_t)heads * 64;
-  a.q_rope_stride_s = 0;
-  a.q_rope_stride_h = 64;
-  a.kv_nope = kv;
-  a.kv_rope = k_pe;
-  a.kv_stride_tok = 512;
-  a.kv_stride_batch = (int64_t)kv_ctx * 512;
-  a.kv_rope_stride_tok = 64;
-  a.kv_rope_stride_batch = (int64_t)kv_ctx * 64;
-  a.block_table = nullptr;
-  a.num_parts = num_parts;
-  a.cache_seqlens = cache_seqlens;
-  a.tile_sched = tile_sched;
-  a.num_splits = num_splits;
-  a.out = out;
-  a.o_stride_b = (int64_t)heads * 512;
-  a.o_stride_s = 0;
-  a.o_stride_h = 512;
-  a.lse = nullptr;
-  a.workspace = workspace;
-  a.workspace_bytes = workspace_bytes;
-  return mla_decode_fwd(&a, stream);
+void mla_launch(const void* Q, const void* Qpe, const void* KV, const void* Kpe, void* glse,
+                void* partial, void* out, int ns) {
+  // The reference's frozen shape: B = 1, H = 16, L = 8192, fp16, contiguous [B, L, 1, D] cache,
+  // sm_scale = 576^-0.5, launched on the null stream.  Caller scratch: glse (fp16
+  // [1, 16, ns + 64]: 32 * (ns + 64) bytes) holds the sequence length, the split prefix sums
+  // and the ns-part tile schedule; partial (fp16 [1, 16, ns, 576]: 18432 * ns bytes) holds the
+  // per-split lse (fp32, padded to 256 bytes) and the 16-bit partial rows [ns, 16, 512].
+  constexpr int kPages = mla::kHandCtx / mla::kPageTokens;
+  if (!Q || !Qpe || !KV || !Kpe || !glse || !partial || !out) {
+    fail(MLA_ERR_INVALID, "mla_launch: a pointer is NULL");
+    return;
+  }
+  if (ns < 1 || ns > kPages) {
+    fail(MLA_ERR_INVALID, "mla_launch: ns must be in [1, 128] (the 8192-token cache has 128 pages)");
+    return;
+  }
+  if (!aligned(Q, 16) || !aligned(Qpe, 16) || !aligned(KV, 16) || !aligned(Kpe, 16) || !aligned(glse, 16) ||
+      !aligned(partial, 16) || !aligned(out, 16)) {
+    fail(MLA_ERR_INVALID, "mla_launch: every buffer must be 16-byte aligned");
+    return;
+  }
+  char* g = (char*)glse;
+  int32_t* seqlens = (int32_t*)g;          // [1]
+  int32_t* splits = (int32_t*)(g + 16);    // [2]
+  int32_t* sched = (int32_t*)(g + 64);     // [ns, 8]: 64 + 32 ns <= 32 (ns + 64) bytes
+  const int64_t lse_bytes = ws_lse_bytes(ns, mla::kHandHeads);  // <= 64 ns + 255
+  mla::KParams k{};
+  k.q_nope = (const uint16_t*)Q;
+  k.q_rope = (const uint16_t*)Qpe;
+  k.q_sb = mla::kHandHeads * 512; k.q_ss = 0; k.q_sh = 512;
+  k.qr_sb = mla::kHandHeads * 64; k.qr_ss = 0; k.qr_sh = 64;
+  k.kv_nope = (const uint16_t*)KV;
+  k.kv_rope = (const uint16_t*)Kpe;
+  k.kv_st = 512; k.kv_sb = (int64_t)mla::kHandCtx * 512;
+  k.kr_st = 64; k.kr_sb = (int64_t)mla::kHandCtx * 64;
+  k.block_table = nullptr;
+  k.num_blocks = 1;
+  k.seqlens = seqlens;
+  k.sched = sched;
+  k.splits = splits;
+  k.out = (uint16_t*)out;
+  k.o_sb = mla::kHandHeads * 512; k.o_ss = 0; k.o_sh = 512;
+  k.lse = nullptr;
+  // lse_bytes + 16 * 512 * 2 * ns <= 18432 ns bytes for every ns >= 1
+  k.ws_lse = (float*)partial;
+  k.ws_o = (float*)((char*)partial + lse_bytes);
+  k.part16 = 1;
+  k.batch = 1;
+  k.s_q = 1;
+  k.heads = mla::kHandHeads;
+  k.rows = mla::kHandHeads;
+  k.causal = 0;
+  k.num_parts = ns;
+  k.scale_log2 = mla::kLog2e / sqrtf((float)MLA_DIM_QK);
+  hipStream_t st = nullptr;
+  hipLaunchKernelGGL(mla::mla_launch_sched_kernel, dim3(1), dim3(64), 0, st, seqlens, sched, splits, ns);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = launch_main_dt<MLA_DTYPE_F16>(pick_variant(k.rows), k, 1, st);
+  if (e != hipSuccess) {
+    fail(MLA_ERR_HIP, std::string("mla_launch: launch failed: ") + hipGetErrorString(e));
+    return;
+  }
+  launch_combine(k, (const uint16_t*)k.ws_o, MLA_DTYPE_F16, 0, st);
 }
 
 int mla_kv_append(const mla_kv_append_args* a, void* stream) {

@@ -47,7 +47,9 @@ CONFIGS = {
     "C2": MlaConfig("C2", batch=64, s_q=1, heads=128, dtype=torch.bfloat16, seqlen=4096),
     "C3": MlaConfig("C3", batch=128, s_q=1, heads=16, dtype=torch.bfloat16,
                     seqlen_groups=[(128, 256, 8192)]),
-    "C4": MlaConfig("C4", batch=32, s_q=2, heads=128, dtype=torch.bfloat16, seqlen=16384),
+    # num_splits >= 8: the combine merges many partial O / LSE tiles per row
+    "C4": MlaConfig("C4", batch=32, s_q=2, heads=128, dtype=torch.bfloat16, seqlen=16384,
+                    num_splits=8),
     "C5": MlaConfig("C5", batch=132, s_q=1, heads=64, dtype=torch.float16, sigma=0.5,
                     seqlen_groups=[(1, 16384), (31, 2048, 8192), (100, 1, 128)]),
 }

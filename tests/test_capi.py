@@ -103,9 +103,23 @@ def test_host_schedule_matches_oracle(seed):
 def test_workspace_bytes(lib):
     n = lib.mla_workspace_bytes(64, 1, 128, 128)
     slots, rows = 64 + 128, 128
-    # fp32 lse per (slot, row) padded to 256 bytes, then 16-bit partial rows of 512
-    assert n == -(-slots * rows * 4 // 256) * 256 + slots * rows * 512 * 2
+    # fp32 lse per (slot, row) padded to 256 bytes, then fp32 partial rows of 512
+    assert n == -(-slots * rows * 4 // 256) * 256 + slots * rows * 512 * 4
     assert lib.mla_workspace_bytes(0, 1, 16, 4) == 0
+
+
+@pytest.mark.parametrize("ptrs, ns, needle", [
+    ((0, 256, 256, 256, 256, 256, 256), 4, b"NULL"),
+    ((256,) * 7, 0, b"ns must be in [1, 128]"),
+    ((256,) * 7, 129, b"ns must be in [1, 128]"),
+    ((256, 256, 8, 256, 256, 256, 256), 4, b"16-byte aligned"),
+])
+def test_mla_launch_rejects_bad_args(lib, ptrs, ns, needle):
+    # The reference's binding (argtypes [c_void_p] * 7 + [c_int], restype None): an invalid call
+    # launches nothing and leaves its reason in mla_last_error.
+    assert lib.mla_launch.restype is None
+    assert lib.mla_launch(*ptrs, ns) is None
+    assert needle in lib.mla_last_error()
 
 
 def test_num_parts(lib):

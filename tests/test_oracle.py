@@ -373,3 +373,32 @@ def test_check_cli_reference_equals_oracle():
         got = torch_ref(q, q_pe, kv, k_pe, b, h, hk, ctx, 512, 64)
         want = R.decode_contiguous(q, q_pe, kv, k_pe)
         assert torch.allclose(got, want, atol=1e-6, rtol=1e-5)
+
+
+def test_bf16_partials_break_the_bar():
+    """Why the decode keeps split partials in fp32.  Outputs in [2, 4) (latent dims drawn in
+    that band) merged from 4 splits: with fp32 partials the error against the fp32 oracle is
+    the output's own bf16 rounding (<= 2^-7 = 0.0078); with partials rounded to bf16 before the
+    merge (the reference's partial format, mla_decode.py:73-74) it passes 1e-2."""
+    g = torch.Generator().manual_seed(3)
+    H, L, S = 16, 1024, 4
+    q = (torch.randn(H, 576, generator=g) * 3).to(torch.bfloat16).double()
+    k = torch.empty(L, 576, dtype=torch.float64)
+    k[:, :512] = (2 + 2 * torch.rand(L, 512, generator=g, dtype=torch.float64)).to(torch.bfloat16).double()
+    k[:, 512:] = torch.randn(L, 64, generator=g, dtype=torch.float64).to(torch.bfloat16).double()
+    s = (q @ k.T) * 576 ** -0.5
+    ref = torch.softmax(s, -1) @ k[:, :512]
+    assert ref.min() >= 2 and ref.max() < 4
+    parts, lses = [], []
+    for c in range(S):  # each split's softmax-normalised output and natural-log lse
+        sl = slice(c * L // S, (c + 1) * L // S)
+        parts.append(torch.softmax(s[:, sl], -1) @ k[sl, :512])
+        lses.append(torch.logsumexp(s[:, sl], -1))
+    part_o, part_l = torch.stack(parts), torch.stack(lses)
+    errs = {}
+    for name, po in (("fp32", part_o.float()), ("bf16", part_o.to(torch.bfloat16).float())):
+        out, lse = R.combine(po, part_l.float())
+        assert (lse.double() - torch.logsumexp(s, -1)).abs().max() < 1e-4
+        errs[name] = (out.to(torch.bfloat16).double() - ref).abs().max().item()
+    assert errs["fp32"] <= 2 ** -7 + 1e-6
+    assert errs["bf16"] > 1e-2
