@@ -35,7 +35,8 @@ from ._lib import (MLA_DIM_QK, MLA_DIM_V, MLA_DTYPE_BF16, MLA_DTYPE_F16, MLA_KV_
 _DTYPES = {torch.bfloat16: MLA_DTYPE_BF16, torch.float16: MLA_DTYPE_F16}
 
 _ws_lock = threading.Lock()
-_workspaces: dict = {}
+_workspaces: dict = {}   # (device index, stream handle) -> the buffer calls on that stream use
+_retired: list = []      # buffers replaced by larger ones, kept alive until the process ends
 
 
 def _stream_ptr(device: torch.device) -> int:
@@ -47,21 +48,31 @@ def _require_gpu(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be a GPU tensor (the decode runs only as HIP kernels)")
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A cached, 256-byte-aligned device workspace of at least ``nbytes`` bytes.
+def workspace(device: torch.device, nbytes: int, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """A cached, 256-byte-aligned device workspace of at least ``nbytes`` bytes for calls
+    queued on ``stream`` (torch's current stream of ``device`` by default).
 
-    Kept per device and grown on demand, so steady-state calls allocate nothing.  Calls
-    that share a device share the buffer; they must be ordered on one stream.
+    One buffer per (device, stream), grown on demand, so steady-state calls allocate nothing:
+    calls on one stream run in order and can share it, calls on different streams never do.
+    A buffer, once handed out, is never freed (a HIP graph captured with its address may
+    replay later): when a call needs more, the old buffer is kept alive until the process ends
+    and a larger one takes its place.  The returned slice's length is the byte count to pass
+    as ``workspace_bytes``.
     """
     nbytes = max(int(nbytes), 256)
-    key = (device.type, device.index)
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, stream.cuda_stream)
     with _ws_lock:
         buf = _workspaces.get(key)
-        if buf is None or buf.numel() < nbytes:
+        if buf is None or buf.numel() - (-buf.data_ptr()) % 256 < nbytes:
+            if buf is not None:
+                _retired.append(buf)
             buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
             _workspaces[key] = buf
     off = (-buf.data_ptr()) % 256
-    return buf[off:off + nbytes]
+    return buf[off:]
 
 
 def num_parts_for(batch: int, s_q: int, heads_q: int, heads_k: int = 1, cu_count: int = 0) -> int:
@@ -245,8 +256,7 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tens
     splits = splits.contiguous()
     num_parts = sched.shape[0]
     lib = _lib.load()
-    ws_bytes = lib.mla_workspace_bytes(B, s_q, H, num_parts)
-    ws = workspace(q.device, ws_bytes)
+    ws = workspace(q.device, lib.mla_workspace_bytes(B, s_q, H, num_parts))
     el = q.element_size()
     a = MlaDecodeArgs()
     a.batch, a.s_q, a.heads_q, a.heads_k = B, s_q, H, 1
@@ -281,7 +291,7 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tens
     a.o_stride_b, a.o_stride_s, a.o_stride_h = out.stride(0), out.stride(1), out.stride(2)
     a.lse = lse.data_ptr()
     a.workspace = ws.data_ptr()
-    a.workspace_bytes = ws_bytes
+    a.workspace_bytes = ws.numel()
     keep = (q, latent, rope, scale, block_table, seqlens, sched, splits, out, lse, ws, indices)
     return a, out, lse, keep
 

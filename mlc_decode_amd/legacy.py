@@ -86,8 +86,7 @@ class MlaKernel:
         seqlens, sched, nsplits = self._schedule(q.device)
         lib = _lib.load()
         num_parts = sched.shape[0]
-        ws_bytes = lib.mla_workspace_bytes(B, 1, H, num_parts)
-        ws = workspace(q.device, ws_bytes)
+        ws = workspace(q.device, lib.mla_workspace_bytes(B, 1, H, num_parts))
         a = MlaDecodeArgs()
         a.batch, a.s_q, a.heads_q, a.heads_k = B, 1, H, 1
         a.dtype = _DTYPES[q.dtype]
@@ -110,6 +109,6 @@ class MlaKernel:
         a.o_stride_b, a.o_stride_s, a.o_stride_h = output.stride(0), 0, output.stride(1)
         a.lse = None
         a.workspace = ws.data_ptr()
-        a.workspace_bytes = ws_bytes
+        a.workspace_bytes = ws.numel()
         check("mla_decode_fwd", lib.mla_decode_fwd(ctypes.byref(a), _stream_ptr(q.device)))
         return output if ret else None

@@ -114,3 +114,44 @@ def test_captured_absorbed_decode(gpu):
         v_e, lse_e = step()
         torch.cuda.synchronize()
         assert torch.equal(v_g, v_e) and torch.equal(lse_g, lse_e), f"replay {rep} differs"
+
+
+def test_graph_replay_after_workspace_growth(gpu):
+    """A graph captured on a stream keeps writing into the workspace it was captured with after a
+    later eager call on that stream needed a larger one: the old buffer is retired, never
+    freed, so a tensor allocated afterwards (the guard) cannot alias it."""
+    from mlc_decode_amd import mla_decode_with_kvcache
+    kv, table, lens = state(5)
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(B, 1, H, 576, generator=g).to(torch.bfloat16).cuda()
+    s = torch.cuda.Stream()
+
+    def step():
+        sched, splits = get_mla_metadata(lens, H, 1)
+        return flash_mla_with_kvcache(q, kv, table, lens, 512, sched, splits, causal=True)
+
+    with torch.cuda.stream(s):
+        out_ref, lse_ref = step()          # creates the workspace of stream s
+    torch.cuda.synchronize()
+    say("capture on a user stream")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out_g, lse_g = step()
+    torch.cuda.synchronize()
+    # a much larger decode on the same stream grows its workspace (B=64, H=128: ~84 MB)
+    Bb, Hb, Lb = 64, 128, 256
+    qb = torch.randn(Bb, 1, Hb, 576, generator=g).to(torch.bfloat16).cuda()
+    kvb = torch.randn(Bb * 4, 64, 1, 576, generator=g).to(torch.bfloat16).cuda()
+    tb = torch.arange(Bb * 4, dtype=torch.int32).reshape(Bb, 4).cuda()
+    lb = torch.full((Bb,), Lb, dtype=torch.int32).cuda()
+    say("grow the workspace eagerly on the same stream")
+    with torch.cuda.stream(s):
+        mla_decode_with_kvcache(qb, kvb, tb, lb)
+    torch.cuda.synchronize()
+    guard = torch.full((96 << 20,), 7, dtype=torch.uint8, device=gpu)
+    for rep in range(3):
+        say(f"replay after growth {rep}")
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_ref) and torch.equal(lse_g, lse_ref), f"replay {rep} differs"
+        assert bool(torch.all(guard == 7)), f"replay {rep} wrote outside its workspace"
