@@ -21,7 +21,7 @@ CASES = [
     # name, B, s_q, H, lengths, dtype, sigma, causal
     ("h16_l1", 1, 1, 16, [1], torch.bfloat16, 1.0, True),
     ("h16_tails", 3, 1, 16, [63, 65, 129], torch.bfloat16, 1.0, True),
-    ("h32_sq2_causal", 3, 2, 16, [1, 2, 97], torch.bfloat16, 1.0, True),
+    ("h16_sq2_causal", 3, 2, 16, [1, 2, 97], torch.bfloat16, 1.0, True),
     ("h64_fp16_ragged", 3, 1, 64, [5, 64, 100], torch.float16, 0.5, True),
     ("h128_sq2", 1, 2, 128, [130], torch.bfloat16, 1.0, True),
     ("h16_sq2_noncausal", 2, 2, 16, [40, 70], torch.float16, 1.0, False),
