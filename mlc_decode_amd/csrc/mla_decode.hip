@@ -29,6 +29,7 @@
 // redo of the segment.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <math.h>
 #include <mutex>
 #include <string>
@@ -1300,6 +1301,573 @@ void mla_splitkv_kernel(KParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// wide kernel: 64 or 128 query rows per workgroup, PV split by output dims
+// ---------------------------------------------------------------------------------------
+// Four waves share a workgroup of R = 64*HT rows.  QK is split by rows: wave w owns rows
+// 16*HT*w .. +16*HT (query fragments resident in VGPRs, S^T in VGPRs).  PV is split by output
+// dims: wave w owns dims 128w .. 128w+127 of all R rows (8 x 4*HT accumulator tiles in AGPRs),
+// so each wave reads only its quarter of V^T from LDS, and every V^T fragment feeds 4*HT
+// MFMAs.  P^T crosses waves through LDS: each wave writes its row tiles' B fragments (one KiB
+// each, lane-linear) and every wave reads all of them.  Iteration k of the stage loop runs QK
+// of stage k, then the softmax of stage k next to PV of stage k-1 (whose P^T all waves wrote
+// during iteration k-1), so a stage stays in LDS for two iterations.  LDS: a latent ring of 4
+// 32-token stages (the stage of PV, the stage of QK, two in flight), a rope ring of 3 (rope is
+// read by QK only), two P^T buffers.
+//
+// Stage layout.  Latent: 32 blocks of 1 KiB, block q*8 + s (row group q = rows 8q .. 8q+7,
+// 128-byte segment s = dims 64s .. 64s+63); rope: 4 blocks, block q.  Inside a block, 16-byte
+// chunk c8 of row r sits at slot 8*(r%8) + (c8 ^ stage_swz(r % 16)) (the layout of the
+// one-ring kernel above, with the rope blocks moved to their own ring).
+constexpr int kWideLat = 4;                  // latent stages resident
+constexpr int kWideRope = 3;                 // rope stages resident
+constexpr int kLatStageBytes = 32 * 1024;    // 32 token rows x 512 dims
+constexpr int kRopeStageBytes = 4 * 1024;    // 32 token rows x 64 dims
+constexpr int kWidePanel = 16 * 1024;        // tokens 16..31 of a latent stage
+
+// Wave w loads row group w of a stage: 8 latent blocks and 1 rope block, each one
+// global_load_lds_dwordx4 whose eight lanes per row cover one 128-byte line.  Rows past the
+// sequence end re-read its last row (in bounds, masked later).
+__device__ __forceinline__ void issue_stage_wide(uint8_t LDS_AS* lat, uint8_t LDS_AS* rope,
+                                                 const uint16_t* nope_base, const uint16_t* rope_base,
+                                                 int kv_st, int kr_st, int last_row, int wave, int lane) {
+  const int q = wave;  // uniform
+  int row = 8 * q + (lane >> 3);
+  row = row < last_row ? row : last_row;
+  const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((q & 1) << 3) | (lane >> 3))) << 4);
+  const uint32_t on = (uint32_t)(row * kv_st) * 2 + cl;
+  const uint32_t orp = (uint32_t)(row * kr_st) * 2 + cl;
+  uint8_t LDS_AS* dst = lat + q * 8 * 1024;
+#pragma unroll
+  for (int sg = 0; sg < 8; ++sg)
+    dma16((const char*)nope_base + 128 * sg, on, (uint32_t)(uintptr_t)(dst + sg * 1024));
+  dma16(rope_base, orp, (uint32_t)(uintptr_t)(rope + q * 1024));
+}
+
+template <int DT, int HT>
+__global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
+  constexpr int NW = 4;
+  constexpr int RT = NW * HT;        // 16-row tiles per workgroup
+  constexpr int R = 16 * RT;         // rows per workgroup
+  constexpr int WDT = 8;             // 16-dim tiles per wave (128 dims)
+  constexpr int DK = 4;              // LDS prefetch depth of the QK A fragments
+  constexpr float kTau = ref_tau<DT>();
+  constexpr int kPBytes = RT * 1024;
+  __shared__ __attribute__((aligned(1024))) uint8_t lat_raw[kWideLat * kLatStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t rope_raw[kWideRope * kRopeStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t pt_raw[2 * kPBytes];
+  __shared__ float inv_sh[R];   // 1 / row sum of every row, for the epilogue
+  // "score above reference" words, one per stage modulo 4 (see the one-ring kernel)
+  __shared__ int over_sh[4];
+  uint8_t LDS_AS* const lat = (uint8_t LDS_AS*)lat_raw;
+  uint8_t LDS_AS* const rope = (uint8_t LDS_AS*)rope_raw;
+  uint8_t LDS_AS* const ptb = (uint8_t LDS_AS*)pt_raw;
+
+  const int part = blockIdx.x;
+  const int hb = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const int li = lane & 15;
+  const int rowb = hb * R;                 // the workgroup's first row (PV rows rowb .. +R)
+  const int row0 = rowb + wave * 16 * HT;  // this wave's QK rows
+
+  const int32_t* rec = p.sched + part * kSchedWords;
+  int b = rec[0];
+  int page = rec[1];
+  const int end_b = rec[2];
+  const int end_page = rec[3];
+  int split = rec[4];
+
+  // Per-lane LDS offsets of the fragments (recomputed each stage from an opaque copy of the
+  // lane id, see the stage loop: kept live across the loop they get spilled, and a reload
+  // before the loop makes the compiler wait for every outstanding stage load inside it).
+  // QK A operand, fragment (kk, tt), kk < 16: token row 16tt + li of latent chunk
+  // sigma(kk, g) = 8*(kk/2) + 2g + kk%2, i.e. block (2tt + li/8)*8 + kk/2, chunk-in-block
+  // 2g + kk%2: lane offset kl[kk%2] plus the immediate tt*16 KiB + (kk/2)*1 KiB.  kk = 16, 17:
+  // the rope chunk 2g + kk%2 of rope block 2tt + li/8: kr[kk%2] + tt*2 KiB.
+  // PV A operand (V^T), dim tile dt = 4s + d4 (segment s, tile d4 in it): the lane addresses
+  // token row rv = 4g + li/4 (and row rv + 16 in the second panel), bytes 32*d4 + 8*(li%4) of
+  // segment s; the swizzle flips only address bits 5-6 with d4, so the address is
+  // (v_lane ^ 32*d4) + 1024*s.  Wave w's segments are 2w and 2w + 1.
+  struct LaneOffsets {
+    int kl0, kl1, kr0, kr1, v;
+  };
+  auto lane_offsets = [&](int ln) __attribute__((always_inline)) {
+    const int gg = ln >> 4, ll = ln & 15;
+    const int sw0 = (((ll & 7) << 3) + ((2 * gg) ^ stage_swz(ll))) << 4;
+    const int sw1 = (((ll & 7) << 3) + ((2 * gg + 1) ^ stage_swz(ll))) << 4;
+    const int r = 4 * gg + (ll >> 2);
+    LaneOffsets o;
+    o.kl0 = (ll >> 3) * 8192 + sw0;
+    o.kl1 = (ll >> 3) * 8192 + sw1;
+    o.kr0 = (ll >> 3) * 1024 + sw0;
+    o.kr1 = (ll >> 3) * 1024 + sw1;
+    o.v = (r >> 3) * 8192 + ((r & 7) << 7) + ((((ll >> 1) & 1) ^ stage_swz(r)) << 4) + ((ll & 1) << 3) + 2048 * wave;
+    return o;
+  };
+
+  const int kv_st = (int)p.kv_st, kr_st = (int)p.kr_st;
+  const bool paged = p.block_table != nullptr;
+
+#pragma unroll 1
+  for (; b < p.batch; ++b, page = 0, split = 0) {
+    if (!(b < end_b || (b == end_b && page < end_page))) break;
+    const int L = p.seqlens[b] > 0 ? p.seqlens[b] : 0;
+    const int np = pages_of(L);
+    const int stop = (b == end_b) ? end_page : np;
+    const int st_begin = 2 * page;
+    const int st_end_seq = (L + kStageTok - 1) / kStageTok;
+    const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
+    const int nst = st_end > st_begin ? st_end - st_begin : 0;
+
+    // ---- query fragments of this wave's rows (B operand of S^T = K Q^T), resident for the
+    // segment; rows past the end re-load the last row (their results are never written)
+    i32x4 qf[HT][kKSteps];
+    int lim[HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      int row = row0 + 16 * ht + li;
+      row = row < p.rows ? row : p.rows - 1;
+      const int s = row / p.heads;
+      const int h = row - s * p.heads;
+      lim[ht] = L - (p.causal ? (p.s_q - 1 - s) : 0);
+      const uint16_t* qn = p.q_nope + (b * p.q_sb + s * p.q_ss + h * p.q_sh) + 16 * g;
+      const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 16 * g;
+#pragma unroll
+      for (int kk = 0; kk < kKSteps; ++kk) {
+        const int d = 64 * (kk >> 1) + 8 * (kk & 1);  // dims 8*sigma(kk, g)
+        qf[ht][kk] = *(const i32x4*)(d < kRopeOff ? qn + d : qr + (d - kRopeOff));
+      }
+    }
+    const int lmin = L - (p.causal ? p.s_q - 1 : 0);  // every row sees tokens < lmin
+
+    f32x4 o[WDT][RT];
+    // row sums of this wave's QK rows: l_part over P as rounded for PV (normalises the
+    // output), l_exact over the fp32 P (gives the lse)
+    float m_ref[HT], l_part[HT], l_exact[HT];
+    int pbase = 0, bt_lane = 0;
+
+    auto load_page_ids = [&](int first) __attribute__((always_inline)) {
+      pbase = first;
+      if (paged) {
+        const int last = np > 0 ? np - 1 : 0;
+        const int pi = pbase + lane < last ? pbase + lane : last;
+        const int v = p.block_table[(int64_t)b * p.bt_stride + pi];
+        bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
+      }
+    };
+    // The loads of one stage: wave w fetches row group w, 8 latent blocks and 1 rope block (one
+    // global_load_lds_dwordx4 each, eight lanes per 128-byte line).  `prepare` does the scalar
+    // work once (page lookup, 32 x 32 -> 64-bit page offset: page strides are below 2^31
+    // elements, checked by the host); `issue_one(si, j)` issues load j, so the nine loads can
+    // be spread between MFMAs (in a burst they hold the wave for ~900 cycles behind the CU's
+    // load path; spread, ~10 each).  Rows past the sequence end re-read its last row.
+    struct StageIssue {
+      const char* nb;   // latent row base of the stage (bytes)
+      const char* rb;   // rope row base
+      uint32_t on, orp; // per-lane byte offsets
+      uint32_t lat_dst, rope_dst;
+    };
+    auto prepare = [&](int k) __attribute__((always_inline)) {
+      const int st = st_begin + k;
+      StageIssue si;
+      const int tok = (st & 1) * kStageTok;
+      if (paged) {
+        const int pidx = st >> 1;
+        if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
+        const uint32_t pg = (uint32_t)__builtin_amdgcn_readlane(bt_lane, pidx - pbase);
+        si.nb = (const char*)p.kv_nope + ((uint64_t)pg * (uint32_t)p.kv_sp + (uint32_t)(tok * kv_st)) * 2;
+        si.rb = (const char*)p.kv_rope + ((uint64_t)pg * (uint32_t)p.kr_sp + (uint32_t)(tok * kr_st)) * 2;
+      } else {
+        si.nb = (const char*)(p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st * kStageTok * kv_st));
+        si.rb = (const char*)(p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st));
+      }
+      const int left = L - st * kStageTok;
+      const int last_row = (left < kStageTok ? left : kStageTok) - 1;
+      int row = 8 * wave + (lane >> 3);
+      row = row < last_row ? row : last_row;
+      const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((wave & 1) << 3) | (lane >> 3))) << 4);
+      si.on = (uint32_t)(row * kv_st) * 2 + cl;
+      si.orp = (uint32_t)(row * kr_st) * 2 + cl;
+      si.lat_dst = (uint32_t)(uintptr_t)(lat + (k % kWideLat) * kLatStageBytes + wave * 8 * 1024);
+      si.rope_dst = (uint32_t)(uintptr_t)(rope + (k % kWideRope) * kRopeStageBytes + wave * 1024);
+      return si;
+    };
+    auto issue_one = [&](const StageIssue& si, int j) __attribute__((always_inline)) {
+      if (j < 8) dma16(si.nb + 128 * j, si.on, si.lat_dst + j * 1024);
+      else dma16(si.rb, si.orp, si.rope_dst);
+    };
+    auto issue = [&](int k) __attribute__((always_inline)) {  // all nine at once
+      const StageIssue si = prepare(k);
+#pragma unroll
+      for (int j = 0; j < 9; ++j) issue_one(si, j);
+    };
+
+    // One pass over the segment's stages; returns true (uniformly) when a first-stage-reference
+    // pass saw a score above its reference by more than tau.
+    //
+    // Iteration k (1 <= k <= nst): wait for stage k, barrier, QK(k) with four of stage k+2's
+    // loads between its MFMAs and, in its last steps, the reads of this wave's V^T fragments of
+    // stage k-1; then PV(k-1) with the softmax of stage k and the other five loads woven into
+    // it.  Iteration 0 (QK and softmax of stage 0) is peeled; the last iteration has no stage to
+    // score and runs the same body with scores of -inf, so PV keeps a single site.
+    auto run_pass = [&](auto mode_tag) __attribute__((always_inline)) -> bool {
+      constexpr int MODE = decltype(mode_tag)::value;
+      constexpr bool kPV = MODE != kPassRowMax;
+      if constexpr (kPV) {
+#pragma unroll
+        for (int t = 0; t < WDT; ++t)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) o[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) l_part[ht] = l_exact[ht] = 0.f;
+      }
+      if constexpr (MODE != kPassFixedRef) {
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) m_ref[ht] = -INFINITY;
+      }
+      if constexpr (MODE == kPassFirstStageRef) {
+        if (wave == 0) over_sh[lane & 3] = 0;  // uniform branch; ordered by the first barrier
+      }
+      load_page_ids(page);
+      wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
+      if (0 < nst) issue(0);
+      if (1 < nst) issue(1);
+
+      // V^T fragment t (t = 2*d4 + sl: segment 2w + sl, tile d4 in it) of stage kp
+      auto v_frag = [&](const uint8_t LDS_AS* vb, int t) __attribute__((always_inline)) {
+        const uint32_t x = (uint32_t)(32 * (t >> 1));
+        const uint8_t LDS_AS* a = x ? (const uint8_t LDS_AS*)(uintptr_t)((uint32_t)(uintptr_t)vb ^ x) : vb;
+        a += (t & 1) * 1024;
+        const i16x4 lo16 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 LDS_AS*)a);
+        const i16x4 hi16 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 LDS_AS*)(a + kWidePanel));
+        const i32x2 lo2 = __builtin_bit_cast(i32x2, lo16);
+        const i32x2 hi2 = __builtin_bit_cast(i32x2, hi16);
+        return i32x4{lo2.x, lo2.y, hi2.x, hi2.y};
+      };
+      auto v_base = [&](int kp, const LaneOffsets& lo) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* vb = lat + (kp % kWideLat) * kLatStageBytes + lo.v;
+        asm volatile("" : "+v"(vb));
+        return vb;
+      };
+
+      // S^T = K Q^T of stage k over 576 dims: two 16-token tiles x HT row tiles, fragment
+      // n = 2*kk + tt, DK fragments in flight.  Loads 0..3 of `si` go out after steps 4, 12, 20
+      // and 28; with `vt`, the V^T fragments of stage k-1 are read during the last 8 steps.
+      auto qk = [&](int k, f32x4 (&acc)[HT][2], const LaneOffsets& lo, const StageIssue& si, bool do_issue,
+                    bool vt, i32x4 (&va)[WDT]) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* lb = lat + (k % kWideLat) * kLatStageBytes;
+        const uint8_t LDS_AS* rbs = rope + (k % kWideRope) * kRopeStageBytes;
+        const uint8_t LDS_AS* kb0 = lb + lo.kl0;
+        const uint8_t LDS_AS* kb1 = lb + lo.kl1;
+        const uint8_t LDS_AS* rb0 = rbs + lo.kr0;
+        const uint8_t LDS_AS* rb1 = rbs + lo.kr1;
+        asm volatile("" : "+v"(kb0));
+        asm volatile("" : "+v"(kb1));
+        asm volatile("" : "+v"(rb0));
+        asm volatile("" : "+v"(rb1));
+        const uint8_t LDS_AS* vb = vt ? v_base(k - 1, lo) : lb;
+#define MLA_WFRAG(N)                                                                                   \
+  ((((N) >> 1) < 16)                                                                                   \
+       ? *(const i32x4 LDS_AS*)((((N) >> 1) & 1 ? kb1 : kb0) + ((N) & 1) * kWidePanel + ((N) >> 2) * 1024) \
+       : *(const i32x4 LDS_AS*)((((N) >> 1) & 1 ? rb1 : rb0) + ((N) & 1) * 2048))
+        i32x4 kf[DK];
+#pragma unroll
+        for (int n = 0; n < DK; ++n) kf[n] = MLA_WFRAG(n);
+#pragma unroll
+        for (int n = 0; n < 2 * kKSteps; ++n) {
+          const i32x4 a = kf[n % DK];
+          if (n + DK < 2 * kKSteps) kf[n % DK] = MLA_WFRAG(n + DK);
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) {
+            if (n < 2)
+              mfma_qk_first<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
+            else
+              mfma_qk<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
+          }
+          if ((n & 7) == 4 && do_issue) issue_one(si, n >> 3);  // loads 0..3
+          if (n >= 2 * kKSteps - WDT && vt) va[n - (2 * kKSteps - WDT)] = v_frag(vb, n - (2 * kKSteps - WDT));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#undef MLA_WFRAG
+        qk_settle(acc[0][0]);
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          if (ht > 0) qk_touch(acc[ht][0]);
+          qk_touch(acc[ht][1]);
+        }
+      };
+
+      // mask tokens past each row's limit (uniform branch: the last stages only), then each
+      // lane's largest scaled score per row tile
+      auto mask_max = [&](int k, f32x4 (&acc)[HT][2], float (&lmx)[HT]) __attribute__((always_inline)) {
+        const int st = st_begin + k;
+        if (st * kStageTok + kStageTok > lmin) {
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) {
+            int rel = lim[ht] - st * kStageTok - 4 * g;
+            asm volatile("" : "+v"(rel));
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (16 * tt + r >= rel) acc[ht][tt][r] = -INFINITY;
+          }
+        }
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          const float v = max3f(max3f(acc[ht][0][0], acc[ht][0][1], acc[ht][0][2]),
+                                max3f(acc[ht][0][3], acc[ht][1][0], acc[ht][1][1]),
+                                max3f(acc[ht][1][2], acc[ht][1][3], -INFINITY));
+          lmx[ht] = v * p.scale_log2;
+        }
+      };
+
+      // P^T = 2^(S^T * scale - m) of stage k as the B fragments of PV, row sums, fragments
+      // published to P^T buffer k%2 (iteration 0 only; later stages go through pv_softmax)
+      auto softmax_publish = [&](int k, const f32x4 (&acc)[HT][2]) __attribute__((always_inline)) {
+        uint8_t LDS_AS* pw = ptb + (k & 1) * kPBytes + lane * 16;
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          const float mu = m_ref[ht] == -INFINITY ? 0.f : m_ref[ht];
+          float pv[2][4];
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pv[tt][r] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu);
+          const i32x4 pb = i32x4{(int)pack2<DT>(pv[0][0], pv[0][1]), (int)pack2<DT>(pv[0][2], pv[0][3]),
+                                 (int)pack2<DT>(pv[1][0], pv[1][1]), (int)pack2<DT>(pv[1][2], pv[1][3])};
+          l_part[ht] = packed_sum<DT>(pb, l_part[ht]);
+          l_exact[ht] += ((pv[0][0] + pv[0][1]) + (pv[0][2] + pv[0][3])) +
+                         ((pv[1][0] + pv[1][1]) + (pv[1][2] + pv[1][3]));
+          *(i32x4 LDS_AS*)(pw + (wave * HT + ht) * 1024) = pb;
+        }
+      };
+
+      // PV of stage kp (O^T += V^T P^T over its 32 tokens: this wave's 8 dim tiles x all RT row
+      // tiles) with the softmax of stage kp + 1 and loads 4..8 of `si` woven in.  Step rt
+      // streams P^T fragment rt (two steps ahead) against the 8 resident V^T fragments `va`
+      // (8 MFMAs), then computes two P elements; the slicing is fixed in source order (one
+      // scheduling barrier per step), which also bounds how many operands are live at once.
+      auto pv_softmax = [&](int kp, const f32x4 (&acc)[HT][2], const i32x4 (&va)[WDT],
+                            const StageIssue& si, bool do_issue) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* pp = ptb + (kp & 1) * kPBytes + lane * 16;
+        asm volatile("" : "+v"(pp));
+        uint8_t LDS_AS* pw = ptb + ((kp + 1) & 1) * kPBytes + lane * 16;
+        float mu[HT];
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) mu[ht] = m_ref[ht] == -INFINITY ? 0.f : m_ref[ht];
+        float pvv[HT][8];
+        // softmax element e of the 8 * HT this lane owns: row tile e / 8, token tile (e / 4) % 2,
+        // token 4g + e % 4 of it
+        auto p_elem = [&](int e) __attribute__((always_inline)) {
+          const int ht = e >> 3, tt = (e >> 2) & 1, r = e & 3;
+          pvv[ht][e & 7] = fast_exp2(acc[ht][tt][r] * p.scale_log2 - mu[ht]);
+        };
+        auto p_finish = [&](int ht) __attribute__((always_inline)) {
+          const float* v = pvv[ht];
+          const i32x4 pb = i32x4{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3]),
+                                 (int)pack2<DT>(v[4], v[5]), (int)pack2<DT>(v[6], v[7])};
+          l_part[ht] = packed_sum<DT>(pb, l_part[ht]);
+          l_exact[ht] += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+          *(i32x4 LDS_AS*)(pw + (wave * HT + ht) * 1024) = pb;
+        };
+        constexpr int kPer = (8 * HT + RT - 1) / RT;  // P elements per step: 2
+        i32x4 bq[2] = {*(const i32x4 LDS_AS*)pp, *(const i32x4 LDS_AS*)(pp + 1024)};
+        i32x4 b_last = bq[0];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const i32x4 bcur = bq[rt & 1];
+          if (rt + 2 < RT) bq[rt & 1] = *(const i32x4 LDS_AS*)(pp + (rt + 2) * 1024);
+#pragma unroll
+          for (int t = 0; t < WDT; ++t) o[t][rt] = mfma32<DT>(va[t], bcur, o[t][rt]);
+#pragma unroll
+          for (int q = 0; q < kPer; ++q) {
+            const int e = rt * kPer + q;
+            if (e < 8 * HT) {
+              p_elem(e);
+              if ((e & 7) == 7) p_finish(e >> 3);
+            }
+          }
+          // loads 4..8 after steps (2i + 1) * RT / 10
+#pragma unroll
+          for (int i = 0; i < 5; ++i)
+            if (rt == (2 * i + 1) * RT / 10 && do_issue) issue_one(si, 4 + i);
+          __builtin_amdgcn_sched_barrier(0);
+          b_last = bcur;
+        }
+        // the last MFMAs still read their operands for several passes after they issue
+        i32x4 v7 = va[WDT - 1];
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(v7), "+v"(b_last));
+      };
+
+      bool abort = false;
+      if (nst > 0) {  // ---- iteration 0: QK and softmax of stage 0, all loads of stage 2
+        if (1 < nst) wait_vmcnt<9>();  // stage 0 landed; stage 1 may stay in flight
+        else wait_vmcnt<0>();
+        wait_lgkm0();
+        lds_barrier();
+        if (2 < nst) issue(2);
+        int ln0 = lane;
+        asm volatile("" : "+v"(ln0));
+        const LaneOffsets lo = lane_offsets(ln0);
+        f32x4 acc[HT][2];
+        i32x4 va_unused[WDT];
+        qk(0, acc, lo, StageIssue{}, false, false, va_unused);
+        float lmx[HT];
+        mask_max(0, acc, lmx);
+        if constexpr (MODE == kPassRowMax) {
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) m_ref[ht] = fmaxf(m_ref[ht], lmx[ht]);
+        } else {
+          if constexpr (MODE == kPassFirstStageRef) {
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) m_ref[ht] = wave_max_g(lmx[ht]);
+          }
+          softmax_publish(0, acc);
+        }
+      }
+      // ---- k = 1 .. nst
+      const int kend = kPV ? nst + 1 : nst;
+#pragma unroll 1
+      for (int k = 1; k < kend; ++k) {
+        const bool has_qk = k < nst;  // uniform
+        if (has_qk) {
+          if (k + 1 < nst) wait_vmcnt<9>();  // stage k landed; stage k+1 may stay in flight
+          else wait_vmcnt<0>();
+        }
+        wait_lgkm0();  // this wave's P^T and flag stores of iteration k-1 have landed
+        lds_barrier();
+        // the flag word of stage k-1 (stage 0 sets the reference and never flags), consumed
+        // after QK; wave 0 clears the word of stage k-2, read by every wave in iteration k-1
+        int flag_word = 0;
+        if constexpr (MODE == kPassFirstStageRef) {
+          flag_word = over_sh[(k - 1) & 3];
+          if (k >= 3 && wave == 0) over_sh[(k - 2) & 3] = 0;
+        }
+        const bool do_issue = k + 2 < nst;  // uniform
+        StageIssue si{};
+        if (do_issue) si = prepare(k + 2);
+        int ln = lane;
+        asm volatile("" : "+v"(ln));  // opaque per iteration: the offsets stay inside the loop
+        const LaneOffsets lo = lane_offsets(ln);
+        f32x4 acc[HT][2];
+        i32x4 va[WDT];
+        if (has_qk) {
+          qk(k, acc, lo, si, do_issue, kPV, va);
+        } else {
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) acc[ht][tt] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+          if constexpr (kPV) {
+            const uint8_t LDS_AS* vb = v_base(k - 1, lo);
+#pragma unroll
+            for (int t = 0; t < WDT; ++t) va[t] = v_frag(vb, t);
+          }
+        }
+        if constexpr (MODE == kPassFirstStageRef) {
+          if (flag_word != 0) {  // uniform: every wave read the same word after the same barrier
+            abort = true;
+            break;
+          }
+        }
+        float lmx[HT];
+        mask_max(k, acc, lmx);
+        if constexpr (MODE == kPassRowMax) {
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) m_ref[ht] = fmaxf(m_ref[ht], lmx[ht]);
+          if (do_issue) {
+#pragma unroll
+            for (int j = 4; j < 9; ++j) issue_one(si, j);
+          }
+          continue;
+        }
+        bool over = false;
+        if constexpr (MODE == kPassFirstStageRef) {
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
+        }
+        if constexpr (kPV) pv_softmax(k - 1, acc, va, si, do_issue);
+        if constexpr (MODE == kPassFirstStageRef) {
+          if (__builtin_amdgcn_ballot_w64(over) != 0) over_sh[k & 3] = 1;  // uniform branch
+        }
+      }
+      wait_vmcnt<0>();  // an abandoned pass may leave stage loads in flight
+      wait_lgkm0();
+      lds_barrier();    // every wave is done with the rings and P^T buffers
+      return abort;
+    };
+
+    if (run_pass(std::integral_constant<int, kPassFirstStageRef>{})) {
+      run_pass(std::integral_constant<int, kPassRowMax>{});
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) m_ref[ht] = wave_max_g(m_ref[ht]);
+      run_pass(std::integral_constant<int, kPassFixedRef>{});
+    }
+
+    // ---- epilogue.  The QK-owning wave finishes its rows' sums, writes their lse and
+    // publishes 1 / (row sum); then every wave normalises its dims of all R rows.  Branch-free
+    // apart from uniform branches; padding rows (past the last row) compute and store the last
+    // row's values.
+    const int slot0 = p.splits[b];
+    const bool single = (p.splits[b + 1] - slot0) == 1;
+    const int64_t slot = slot0 + split;
+    int lane_e = lane;
+    asm volatile("" : "+v"(lane_e));
+    const int li_e = lane_e & 15, g_e = lane_e >> 4;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      const float l = wave_sum_g(l_part[ht]);
+      const float lx = wave_sum_g(l_exact[ht]);
+      int row = row0 + 16 * ht + li_e;
+      row = row < p.rows ? row : p.rows - 1;
+      inv_sh[wave * 16 * HT + 16 * ht + li_e] = l > 0.f ? 1.f / l : 0.f;  // four lane groups, one value
+      const float lse2 = lx > 0.f ? m_ref[ht] + __log2f(lx) : -INFINITY;
+      const int s = row / p.heads;
+      const int h = row - s * p.heads;
+      if (single) {
+        if (p.lse != nullptr) p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
+      } else {
+        p.ws_lse[slot * p.rows + row] = lse2;
+      }
+    }
+    wait_lgkm0();
+    lds_barrier();
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const float inv = inv_sh[16 * rt + li];
+      int row = rowb + 16 * rt + li_e;
+      row = row < p.rows ? row : p.rows - 1;
+      if (single) {  // uniform
+        const int s = row / p.heads;
+        const int h = row - s * p.heads;
+        uint16_t* dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 128 * wave + 4 * g_e;
+#pragma unroll
+        for (int t = 0; t < WDT; ++t) {  // dims 128w + 64*(t%2) + 16*(t/2) + 4g ..
+          const f32x4 v = o[t][rt] * inv;
+          *(i32x2*)(dst + 64 * (t & 1) + 16 * (t >> 1)) =
+              i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
+        }
+      } else if (p.part16) {  // uniform
+        uint16_t* dst = (uint16_t*)p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * g_e;
+#pragma unroll
+        for (int t = 0; t < WDT; ++t) {
+          const f32x4 v = o[t][rt] * inv;
+          *(i32x2*)(dst + 64 * (t & 1) + 16 * (t >> 1)) =
+              i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
+        }
+      } else {
+        float* dst = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * g_e;
+#pragma unroll
+        for (int t = 0; t < WDT; ++t) *(f32x4*)(dst + 64 * (t & 1) + 16 * (t >> 1)) = o[t][rt] * inv;
+      }
+    }
+    // inv_sh is rewritten only after the next segment's barriers
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // paged KV-cache append: one wave per sequence (its length is read once, before its rows are
 // written, and advanced after them); lanes 0..63 copy the 512 latent dims and lanes 0..7
 // the 64 rope dims of each new row, 16 bytes per lane
@@ -1926,6 +2494,24 @@ hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) 
   return hipGetLastError();
 }
 
+// The 64- and 128-row dense decodes run the wide kernel (PV split by dims across the waves)
+// unless MLA_WIDE=0 selects the one-ring four-wave kernel (kept for the fp8 and sparse paths).
+bool wide_enabled() {
+  static std::once_flag once;
+  static bool on = true;
+  std::call_once(once, [] {
+    const char* e = getenv("MLA_WIDE");
+    on = !(e != nullptr && e[0] == '0');
+  });
+  return on;
+}
+
+template <int DT, int HT>
+hipError_t launch_wide(const mla::KParams& kp, int head_blocks, hipStream_t st) {
+  hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT>), dim3(kp.num_parts, head_blocks), dim3(256), 0, st, kp);
+  return hipGetLastError();
+}
+
 template <int DT>
 hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blocks, hipStream_t st) {
   if (kp.indices != nullptr) {  // sparse (top-k) decode
@@ -1952,6 +2538,7 @@ hipError_t launch_main_dt(const Variant& v, const mla::KParams& kp, int head_blo
   }
   if (v.ws) return launch_main<DT, 4, 1, 1, true>(kp, head_blocks, st);
   if (v.nw == 1) return launch_main<DT, 1, 2, 1, false>(kp, head_blocks, st);
+  if (wide_enabled()) return v.ht == 1 ? launch_wide<DT, 1>(kp, head_blocks, st) : launch_wide<DT, 2>(kp, head_blocks, st);
   if (v.ht == 1) return launch_main<DT, 4, 1, 4, false>(kp, head_blocks, st);
   return launch_main<DT, 4, 2, 3, false>(kp, head_blocks, st);
 }
@@ -1982,6 +2569,9 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
   if (a->block_table) {
     if (a->kv_stride_page < 0 || a->kv_stride_page % 8 || a->kv_rope_stride_page < 0 || a->kv_rope_stride_page % 8)
       return fail(MLA_ERR_INVALID, "page strides must be non-negative multiples of 8 elements");
+    // page offsets are formed as page id (< 2^31) x 32-bit stride in 64 bits
+    if (a->kv_stride_page >= (int64_t(1) << 32) || a->kv_rope_stride_page >= (int64_t(1) << 32))
+      return fail(MLA_ERR_UNSUPPORTED, "page strides must be below 2^32 elements");
     if (a->block_table_stride < 1) return fail(MLA_ERR_INVALID, "block_table_stride must be >= 1");
     if (a->num_blocks < 1) return fail(MLA_ERR_INVALID, "num_blocks must be >= 1");
   } else {

@@ -336,6 +336,35 @@ def test_reference_contiguous_layout(gpu, kv_ctx, monkeypatch):
     assert_parity(baseline_mla.ref_program(*args), None, ref, None, "ref_program")
 
 
+@pytest.mark.parametrize("kv_ctx", [100, 4096])
+def test_reference_factories_and_run_kernel(gpu, kv_ctx, monkeypatch):
+    """The explicit-config factories (mla_decode.py:33-39, :263; called by
+    scripts/bench_mla_heads.py:130-136 with TileLang knobs) and run_kernel (:715-717)."""
+    import mla_decode
+    monkeypatch.setattr(mla_decode, "_AUTOTUNE_ENABLED", False)
+    g = torch.Generator().manual_seed(kv_ctx + 1)
+    b, h = 2, 64
+    mk = lambda *s: (torch.randn(*s, generator=g) * 0.1).to(torch.float16)  # noqa: E731
+    q, q_pe, kv, k_pe = mk(b, h, 512), mk(b, h, 64), mk(b, kv_ctx, 1, 512), mk(b, kv_ctx, 1, 64)
+    ref = R.decode_contiguous(q, q_pe, kv, k_pe)
+    args = [t.to(gpu) for t in (q, q_pe, kv, k_pe)]
+    scale = 576 ** -0.5
+    for name, factory in (("flashattn_shared_q", mla_decode.flashattn_shared_q),
+                          ("flashattn_frag_q", mla_decode.flashattn_frag_q)):
+        for num_split in (1, 4):
+            kern = factory(b, h, 1, kv_ctx, 512, 64, 64, 64, num_split, 2, 8, scale, threads=256)
+            say(f"{name} kv_ctx={kv_ctx} num_split={num_split}")
+            out = torch.empty_like(args[0])
+            assert kern(*args, out) is None
+            torch.cuda.synchronize()
+            assert_parity(out, None, ref, None, f"{name} ns={num_split}")
+    say(f"run_kernel kv_ctx={kv_ctx}")
+    out = torch.empty_like(args[0])
+    mla_decode.run_kernel(*args, out, b, h, 1, kv_ctx, 512, 64)
+    torch.cuda.synchronize()
+    assert_parity(out, None, ref, None, "run_kernel")
+
+
 def test_reference_autotune_path(gpu):
     import mla_decode
     say("mla_decode._get_kernel autotune b=2 h=64 ctx=1500")
