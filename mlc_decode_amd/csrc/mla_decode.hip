@@ -2277,98 +2277,254 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
 }
 
 // ---------------------------------------------------------------------------------------
-// tile schedule on the device: one workgroup.  Pages staged in LDS and summed; each candidate
-// payload is tested by one thread (a serial pass over the sequences with the closed-form
-// packing step), which also records the packing state at the start of each of 256 sequence
-// chunks; then every thread replays its own chunk from that state and writes the records of
-// the parts that begin in it, so the records are written in parallel.  Produces exactly the
-// host schedule (same packing functions).
+// tile schedule on the device: one workgroup of four waves.
+//   1. page counts (coalesced) and their block-wide prefix sums of pages + f (32-bit while
+//      the total is below 2^30);
+//   2. one wave per candidate payload walks the sequences in windows of 64 (mla_sched.h's
+//      closed form gives the packing state between resets): every lane looks up to 8
+//      sequences ahead for the reset that would follow it, the wave follows these links from
+//      reset to reset with scalar reads, and a ballot over the window finds the next reset
+//      where a link is missing.  It records the state at every window start and the window's
+//      reset lanes;
+//   3. each wave takes whole windows: every lane rebuilds the state entering its sequence from
+//      the window's record (last reset below it, a wave prefix sum of the part increments)
+//      and writes the records of the parts that begin inside it.
+// With no pages at all or a total of 2^30 pages or more, a serial pass per candidate replaces
+// steps 2 and 3.  Either way the schedule is exactly the host's.  Forced splits: slot counts,
+// their prefix sums, one thread per record.
 // ---------------------------------------------------------------------------------------
 constexpr int kMetaMaxBatch = 16384;
 constexpr int kMetaThreads = 256;
+constexpr int kMetaWaves = kMetaThreads / 64;
 constexpr int kMetaMaxCand = 8;
+constexpr int kMetaMaxWin = kMetaMaxBatch / kWalkWin;
+static_assert(kWalkWin == 64, "a walk window is one wave");
+
+// Exclusive prefix over the workgroup of one int64 per thread (and the total).
+__device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* wsum_sh, int64_t* total) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  int64_t inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t o = __shfl_up(inc, off);
+    if (lane >= off) inc += o;
+  }
+  if (lane == 63) wsum_sh[wave] = inc;
+  __syncthreads();
+  int64_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kMetaWaves; ++w) {
+    const int64_t x = wsum_sh[w];
+    before += w < wave ? x : 0;
+    all += x;
+  }
+  __syncthreads();  // wsum_sh is free again
+  *total = all;
+  return before + inc - v;
+}
+
+// Inclusive prefix of one int over the wave.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(v, off);
+    if (lane >= off) v += o;
+  }
+  return v;
+}
+
+// Orders this wave's LDS accesses across lanes: a wave-scope fence (waits for the wave's LDS
+// operations) and a code-motion barrier, so a lane may read what other lanes just wrote.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The walk of one candidate payload T by one wave (S: prefix sums in LDS, batch + 1 entries;
+// sig: the wave's scratch for kWalkWin + kWalkLook residues).  Writes the window entries and
+// reset masks; returns the final part index, -1 if T cannot place a sequence (c < 1).  The
+// same steps as walk_payload_host in mla_sched.h; the lookahead runs on every lane at once,
+// without branches.
+__device__ int walk_payload_wave(const int32_t* S, int batch, int T, int f, WalkEntry* ent, uint64_t* msk,
+                                 int* sig) {
+  const int lane = threadIdx.x & 63;
+  const int c = T - f;
+  if (c < 1) return -1;
+  const uint32_t cu = (uint32_t)c;
+  const int f1 = (int)((uint32_t)(f + 1) % cu);
+  int rs = 0, rsig = 0, p = 0, w = 0;  // last reset: prefix, residue, the part it opened; resets
+  int pend = -1, pend_inc = 0;         // a reset in the next window, reached by a link
+  const int nwin = (batch + kWalkWin - 1) / kWalkWin;
+#pragma unroll 1
+  for (int win = 0; win < nwin; ++win) {
+    const int base = win * kWalkWin;
+    if (lane == 0) ent[win] = WalkEntry{rs, p, w};
+    const int i = base + lane;
+    const bool in = i < batch;
+    const int Si = S[in ? i : batch];
+    const int Sn = S[in ? i + 1 : batch];
+    const int si = (int)((uint32_t)Si % cu);
+    wave_lds_sync();  // the previous window's reads of sig are done
+    sig[lane] = si;
+    if (lane < kWalkLook) {
+      const int k = base + kWalkWin + lane;
+      sig[kWalkWin + lane] = (int)((uint32_t)S[k < batch ? k : batch] % cu);
+    }
+    wave_lds_sync();  // other lanes' residues are visible
+    // lookahead of every lane: all operands loaded first, then a branch-free test per step
+    int Sv[kWalkLook + 1], sv[kWalkLook];
+#pragma unroll
+    for (int d = 0; d <= kWalkLook; ++d) Sv[d] = S[min(i + 1 + d, batch)];  // S[i+1 .. i+9]
+#pragma unroll
+    for (int d = 0; d < kWalkLook; ++d) sv[d] = sig[lane + 1 + d];
+    int d_l = 0, a_l = 0;
+#pragma unroll
+    for (int d = 1; d <= kWalkLook; ++d) {
+      const int Sk = Sv[d - 1], Skn = Sv[d];
+      const int A = Sk - Si;
+      const int e2 = mod_sub(mod_sub(sv[d - 1], si, c), f1, c);
+      const int rem = A <= T ? T - A : c - 1 - e2;
+      const bool hit = (d_l == 0) & (i + d < batch) & (rem <= f) & (rem < Skn - Sk);
+      d_l = hit ? d : d_l;
+      a_l = hit ? A : a_l;
+    }
+    const int inc_l = d_l > 0 ? walk_parts(a_l, T, f, c) + 1 : 0;
+    uint64_t mask = 0;
+    int cur = -1;  // lane of the last reset in this window (wave-uniform)
+    if (pend >= 0) {
+      cur = pend;
+      p += pend_inc;
+      w += 1;
+      mask |= 1ull << cur;
+      pend = -1;
+    }
+#pragma unroll 1
+    for (;;) {
+      int from = 0;
+      if (cur >= 0) {
+        int d = __builtin_amdgcn_readlane(d_l, cur);
+#pragma unroll 1
+        while (d > 0 && cur + d < kWalkWin) {
+          p += __builtin_amdgcn_readlane(inc_l, cur);
+          w += 1;
+          cur += d;
+          mask |= 1ull << cur;
+          d = __builtin_amdgcn_readlane(d_l, cur);
+        }
+        rs = __builtin_amdgcn_readlane(Si, cur);
+        rsig = __builtin_amdgcn_readlane(si, cur);
+        if (d > 0) {
+          pend = cur + d - kWalkWin;
+          pend_inc = __builtin_amdgcn_readlane(inc_l, cur);
+          break;
+        }
+        from = cur + kWalkLook + 1;
+      }
+      if (from >= kWalkWin) break;
+      const int A = Si - rs;
+      const int e2 = mod_sub(mod_sub(si, rsig, c), f1, c);
+      const int rem = A <= T ? T - A : c - 1 - e2;
+      const bool r = in & (i > 0) & (lane >= from) & (rem <= f) & (rem < Sn - Si);
+      const uint64_t m = __ballot(r);
+      if (m == 0) break;
+      cur = __builtin_ctzll(m);
+      const int Sj = __builtin_amdgcn_readlane(Si, cur);
+      p += walk_parts(Sj - rs, T, f, c) + 1;
+      w += 1;
+      rs = Sj;
+      rsig = __builtin_amdgcn_readlane(si, cur);
+      mask |= 1ull << cur;
+    }
+    if (lane == 0) msk[win] = mask;
+  }
+  return p + walk_parts(S[batch] - rs, T, f, c);
+}
 
 __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
     const int32_t* __restrict__ seqlens, int batch, int num_parts, int f, int min_payload,
     int forced, int32_t* __restrict__ sched, int32_t* __restrict__ splits) {
-  __shared__ int32_t pg_sh[kMetaMaxBatch];
-  __shared__ PackState st_sh[kMetaMaxCand][kMetaThreads];
+  // page counts; on the walk path overwritten in place by the exclusive prefix of pages + f
+  __shared__ int32_t s_sh[kMetaMaxBatch + 1];
+  // walk: entries and reset masks per candidate and window; serial pass: the packing state per
+  // candidate at every chunk start (never live together)
+  constexpr int kWalkBytes = kMetaMaxCand * kMetaMaxWin * (int)(sizeof(WalkEntry) + sizeof(uint64_t));
+  constexpr int kSerialBytes = kMetaMaxCand * kMetaThreads * (int)sizeof(PackState);
+  __shared__ __attribute__((aligned(16))) uint8_t u_sh[kWalkBytes > kSerialBytes ? kWalkBytes : kSerialBytes];
+  uint64_t (*msk_sh)[kMetaMaxWin] = reinterpret_cast<uint64_t (*)[kMetaMaxWin]>(u_sh);
+  WalkEntry (*ent_sh)[kMetaMaxWin] =
+      reinterpret_cast<WalkEntry (*)[kMetaMaxWin]>(u_sh + kMetaMaxCand * kMetaMaxWin * sizeof(uint64_t));
+  PackState (*st_sh)[kMetaThreads] = reinterpret_cast<PackState (*)[kMetaThreads]>(u_sh);
   __shared__ PackState fin_sh[kMetaMaxCand];
-  __shared__ int64_t red_sh[kMetaThreads / 64];
+  __shared__ int64_t red_sh[kMetaWaves];
+  __shared__ int flag_sh[kMetaWaves];
+  __shared__ int sig_sh[kMetaWaves][kWalkWin + kWalkLook];  // each wave's residues (walk)
   __shared__ int ok_sh[kMetaMaxCand];
+  __shared__ int last_sh[kMetaMaxCand];
   __shared__ int last_part_sh;
   const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+
+  for (int i = t; i < batch; i += kMetaThreads) s_sh[i] = pages_of(seqlens[i]);
+  __syncthreads();
+  // each thread's contiguous chunk of sequences (for the prefix sums)
+  const int chunk = (batch + kMetaThreads - 1) / kMetaThreads;
+  const int b0 = min(batch, t * chunk), b1 = min(batch, b0 + chunk);
+
   if (forced > 0) {
-    for (int i = t; i < batch; i += kMetaThreads) pg_sh[i] = seqlens[i];
-    __syncthreads();
-    if (t == 0) schedule_forced(pg_sh, batch, forced, sched, splits);
+    int64_t cnt = 0;
+    for (int b = b0; b < b1; ++b) cnt += forced_count(s_sh[b], forced);
+    int64_t slots;
+    int64_t cum = block_exclusive_scan(cnt, red_sh, &slots);
+    if (t == 0) splits[0] = 0;
+    for (int b = b0; b < b1; ++b) {
+      cum += forced_count(s_sh[b], forced);
+      splits[b + 1] = (int32_t)cum;
+    }
+    const int nrec = batch * forced;  // == num_parts (host-checked)
+    for (int r = t; r < nrec; r += kMetaThreads) {
+      const int b = r / forced;
+      forced_record(b, r - b * forced, s_sh[b], forced, sched);
+    }
     return;
   }
-  int64_t part_total = 0;
-  for (int i = t; i < batch; i += kMetaThreads) {
-    const int n = pages_of(seqlens[i]);
-    pg_sh[i] = n;
-    part_total += n + f;
+
+  // chunk sums fit 31 bits (<= 64 sequences of < 2^25 pages); a chunk of 2^22 or more may
+  // take the total past 2^30, which routes to the serial pass (64-bit where needed)
+  int cost = 0, any = 0;
+  for (int b = b0; b < b1; ++b) {
+    cost += s_sh[b] + f;
+    any |= s_sh[b];
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) part_total += __shfl_xor(part_total, off);
-  if ((t & 63) == 0) red_sh[t >> 6] = part_total;
+  const int flags = (any != 0 ? 1 : 0) | (cost >= (1 << 22) ? 2 : 0);
+  int incl = wave_inclusive_scan(cost);
+  const int wflags = (__ballot(flags & 1) != 0 ? 1 : 0) | (__ballot(flags & 2) != 0 ? 2 : 0);
+  if (lane == 63) {
+    red_sh[wave] = incl;
+    flag_sh[wave] = wflags;
+  }
   __syncthreads();
-  int64_t total = 0;
+  int before = incl - cost, total32 = 0, all_flags = 0;
 #pragma unroll
-  for (int w = 0; w < kMetaThreads / 64; ++w) total += red_sh[w];
+  for (int w = 0; w < kMetaWaves; ++w) {
+    before += w < wave ? (int)red_sh[w] : 0;
+    total32 += (int)red_sh[w];
+    all_flags |= flag_sh[w];
+  }
+  const bool walk = all_flags == 1;  // pages somewhere, total below 2^30
+  int64_t total = total32;
+  if (!walk) {
+    __syncthreads();  // red_sh is reused
+    int64_t b64;
+    block_exclusive_scan(cost, red_sh, &b64);
+    total = b64;
+  }
   int64_t lo, hi;
   payload_bounds(total, num_parts, f, &lo, &hi);
   const int ncand = min_payload ? (int)(hi - lo) + 1 : 1;  // <= kMetaMaxCand (host-checked)
-  const int chunk = (batch + kMetaThreads - 1) / kMetaThreads;
-  const int nchunks = (batch + chunk - 1) / chunk;  // chunks that hold sequences, <= kMetaThreads
-  if (t < ncand) {
-    // The serial pass: one sequence after another, the next one's page count read from LDS
-    // while this one is packed (the chain is otherwise one LDS latency per sequence).  While
-    // every quantity fits 31 bits (any real cache: total < 2^30 pages) the step runs in
-    // 32-bit arithmetic (pack_sequence32, the same rule); otherwise in 64-bit.
-    const int64_t T = min_payload ? lo + t : hi;
-    PackState st{T, 0, 0};
-    bool ok = true;
-    int n_next = pg_sh[0];
-    if (total < (1ll << 30)) {
-      int remain = (int)T, part = 0, cum = 0;
-      for (int c = 0; c < nchunks; ++c) {
-        st_sh[t][c] = PackState{remain, part, cum};
-        const int e = min(batch, (c + 1) * chunk);
-        for (int b = c * chunk; b < e; ++b) {
-          const int n = n_next;
-          n_next = pg_sh[b + 1 < batch ? b + 1 : b];
-          if (ok) ok = pack_sequence32(n, (int)T, f, remain, part, cum) && part < num_parts;
-        }
-      }
-      st = PackState{remain, part, cum};
-    } else {
-      for (int c = 0; c < nchunks; ++c) {
-        st_sh[t][c] = st;
-        const int e = min(batch, (c + 1) * chunk);
-        for (int b = c * chunk; b < e; ++b) {
-          const int n = n_next;
-          n_next = pg_sh[b + 1 < batch ? b + 1 : b];
-          if (ok) ok = pack_sequence(b, n, T, f, st, NoEmit{}) && st.part < num_parts;
-        }
-      }
-    }
-    fin_sh[t] = st;  // the state every empty chunk starts (and ends) in
-    ok_sh[t] = ok ? 1 : 0;
-  }
-  __syncthreads();
   int best = ncand - 1;  // the largest candidate (hi) always fits
-  for (int i = ncand - 1; i >= 0; --i)
-    if (ok_sh[i]) best = i;
-  const int64_t T = min_payload ? lo + best : hi;
-  PackState st = t < nchunks ? st_sh[best][t] : fin_sh[best];
-  if (t == 0) {  // part 0 begins at the first page; its end is written by whoever closes it
-    sched[0] = 0;
-    sched[1] = 0;
-    sched[4] = 0;
-    splits[0] = 0;
-  }
+  int64_t T;
   const auto emit = [&](int p, int b, int page, int split) {
     if (p < num_parts) {
       int32_t* rec = sched + p * kSchedWords;
@@ -2381,12 +2537,104 @@ __global__ __launch_bounds__(kMetaThreads) void mla_metadata_kernel(
       sched[(p - 1) * kSchedWords + 3] = page;
     }
   };
-  const int e = min(batch, (t + 1) * chunk);
-  for (int b = t * chunk; b < e; ++b) {
-    pack_sequence(b, pg_sh[b], T, f, st, emit);
-    splits[b + 1] = st.cum;
+  if (t == 0) {  // part 0 begins at the first page; its end is written by whoever closes it
+    sched[0] = 0;
+    sched[1] = 0;
+    sched[4] = 0;
+    splits[0] = 0;
   }
-  if (t == kMetaThreads - 1) last_part_sh = st.part;  // the last chunk ends at the final state
+
+  if (walk) {
+    // ---- prefix sums in place (each thread owns its chunk)
+    int run = before;
+    for (int b = b0; b < b1; ++b) {
+      const int n = s_sh[b];
+      s_sh[b] = run;
+      run += n + f;
+    }
+    if (t == 0) s_sh[batch] = total32;
+    __syncthreads();
+    for (int ci = wave; ci < ncand; ci += kMetaWaves) {  // uniform per wave
+      const int fin = walk_payload_wave(s_sh, batch, (int)(min_payload ? lo + ci : hi), f, ent_sh[ci], msk_sh[ci],
+                                        sig_sh[wave]);
+      if (lane == 0) {
+        ok_sh[ci] = fin >= 0 && fin < num_parts;
+        last_sh[ci] = fin;
+      }
+    }
+    __syncthreads();
+    for (int i = ncand - 1; i >= 0; --i)
+      if (ok_sh[i]) best = i;
+    T = min_payload ? lo + best : hi;
+    const int Tb = (int)T, c = Tb - f;
+    const int nwin = (batch + kWalkWin - 1) / kWalkWin;
+    for (int win = wave; win < nwin; win += kMetaWaves) {  // uniform per wave
+      const int m = win * kWalkWin + lane;
+      const bool in = m < batch;
+      const WalkEntry e = ent_sh[best][win];
+      const uint64_t mask = msk_sh[best][win];
+      const uint64_t below = mask & ((1ull << lane) - 1);
+      const int Sm = in ? s_sh[m] : 0;
+      const int Sprev = below != 0 ? s_sh[win * kWalkWin + 63 - __builtin_clzll(below)] : e.rs;
+      const int inc = ((mask >> lane) & 1) ? walk_parts(Sm - Sprev, Tb, f, c) + 1 : 0;
+      const int pinc = wave_inclusive_scan(inc);  // part increments of the resets up to this lane
+      if (in) {
+        const int A = Sm - Sprev;
+        int part = e.p + pinc - inc + walk_parts(A, Tb, f, c);
+        int remain = walk_remain(A, Tb, f, c);
+        int cum = part + m - (e.w + __builtin_popcountll(below));
+        pack_sequence_emit32(m, s_sh[m + 1] - Sm - f, Tb, f, remain, part, cum, emit);
+        splits[m + 1] = cum;
+      }
+    }
+    if (t == 0) last_part_sh = last_sh[best];
+  } else {
+    // ---- serial pass per candidate (s_sh holds page counts)
+    const int nchunks = (batch + chunk - 1) / chunk;  // chunks that hold sequences, <= kMetaThreads
+    if (t < ncand) {
+      // one sequence after another, the next one's page count read from LDS while this one is
+      // packed; 32-bit steps while every quantity fits 31 bits, else 64-bit
+      const int64_t Tc = min_payload ? lo + t : hi;
+      PackState st{Tc, 0, 0};
+      bool ok = true;
+      int n_next = s_sh[0];
+      if (total < (1ll << 30)) {
+        int remain = (int)Tc, part = 0, cum = 0;
+        for (int c = 0; c < nchunks; ++c) {
+          st_sh[t][c] = PackState{remain, part, cum};
+          const int e = min(batch, (c + 1) * chunk);
+          for (int b = c * chunk; b < e; ++b) {
+            const int n = n_next;
+            n_next = s_sh[b + 1 < batch ? b + 1 : b];
+            if (ok) ok = pack_sequence32(n, (int)Tc, f, remain, part, cum) && part < num_parts;
+          }
+        }
+        st = PackState{remain, part, cum};
+      } else {
+        for (int c = 0; c < nchunks; ++c) {
+          st_sh[t][c] = st;
+          const int e = min(batch, (c + 1) * chunk);
+          for (int b = c * chunk; b < e; ++b) {
+            const int n = n_next;
+            n_next = s_sh[b + 1 < batch ? b + 1 : b];
+            if (ok) ok = pack_sequence(b, n, Tc, f, st, NoEmit{}) && st.part < num_parts;
+          }
+        }
+      }
+      fin_sh[t] = st;  // the state every empty chunk starts (and ends) in
+      ok_sh[t] = ok ? 1 : 0;
+    }
+    __syncthreads();
+    for (int i = ncand - 1; i >= 0; --i)
+      if (ok_sh[i]) best = i;
+    T = min_payload ? lo + best : hi;
+    PackState st = t < nchunks ? st_sh[best][t] : fin_sh[best];
+    for (int b = b0; b < b1; ++b) {
+      pack_sequence(b, s_sh[b], T, f, st, emit);
+      splits[b + 1] = st.cum;
+    }
+    if (t == kMetaThreads - 1) last_part_sh = st.part;  // the last chunk ends at the final state
+  }
   __syncthreads();
   const int last = last_part_sh;
   for (int p = t; p < num_parts; p += kMetaThreads) {

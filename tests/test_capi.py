@@ -366,3 +366,54 @@ def test_pack_sequence32_equals_pack_sequence(tmp_path):
                     "-I", os.path.join(repo, "mlc_decode_amd", "csrc"), "-o", str(exe), str(src)], check=True)
     bad, steps = map(int, subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split())
     assert steps > 100000 and bad == 0
+
+
+_WALK_PROG = r"""
+#include <cstdio>
+#include <cstdint>
+#include <vector>
+#include "mla_sched.h"
+using namespace mla;
+int main() {
+  uint64_t x = 0x9E3779B97F4A7C15ull;
+  auto rnd = [&](int m) { x ^= x << 13; x ^= x >> 7; x ^= x << 17; return (int)(x % (uint64_t)m); };
+  long bad = 0, walked = 0;
+  for (int trial = 0; trial < 20000; ++trial) {
+    const int B = 1 + (trial % 5 == 0 ? rnd(700) : rnd(140));
+    std::vector<int32_t> L(B);
+    for (auto& l : L) {
+      const int r = rnd(10);
+      l = r == 0 ? 0 : r == 1 ? 1 + rnd(64) : trial % 4 == 0 ? rnd(300000) : trial % 4 == 1 ? 4096 : rnd(20000);
+    }
+    const int parts = 1 + rnd(trial % 3 == 0 ? 8 : 1100), f = rnd(8);
+    for (int mp = 0; mp < 2; ++mp) {
+      const int nw = (B + kWalkWin - 1) / kWalkWin;
+      std::vector<int32_t> pg(B), s1(parts * 8, -7), n1(B + 1, -7), s2(parts * 8, -7), n2(B + 1, -7), S(B + 1);
+      std::vector<WalkEntry> ent(8 * nw);
+      std::vector<uint64_t> msk(8 * nw);
+      schedule_packed(L.data(), B, parts, f, mp, pg.data(), s1.data(), n1.data());
+      if (schedule_walk_host(L.data(), B, parts, f, mp, S.data(), ent.data(), msk.data(), s2.data(), n2.data()) < 0)
+        continue;
+      ++walked;
+      if (s1 != s2 || n1 != n2) ++bad;
+    }
+  }
+  std::printf("%ld %ld\n", bad, walked);
+  return 0;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++ to build the schedule header")
+def test_walk_schedule_equals_serial_packing(tmp_path):
+    # the closed form between resets (the device's parallel schedule, emulated on the host with
+    # the same windows, entries and masks) against the serial greedy packing, on random
+    # batches with empty and one-page sequences, tiny payloads (c = T - f < 1) and f = 0 .. 7
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = tmp_path / "walk.cpp"
+    src.write_text(_WALK_PROG)
+    exe = tmp_path / "walk"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", os.path.join(repo, "include"),
+                    "-I", os.path.join(repo, "mlc_decode_amd", "csrc"), "-o", str(exe), str(src)], check=True)
+    bad, walked = map(int, subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split())
+    assert walked > 30000 and bad == 0

@@ -252,6 +252,9 @@ def test_schedule_device_matches_host(gpu):
         [rng.choice([0, 1, 64, rng.randint(1, 9000)]) for _ in range(700)],
         [rng.randint(0, 3000) for _ in range(257)],   # two sequences per chunk, 129 chunks
         [5],
+        [rng.randint(1, 200000) for _ in range(16384)],  # the largest batch: 256 walk windows
+        [0] * 300,                                      # no pages: the serial pass
+        [2**31 - 64] * 40,                              # 2^31 pages in total: the 64-bit serial pass
     ]
     for lengths in cases:
         seq = torch.tensor(lengths, dtype=torch.int32, device=gpu)
