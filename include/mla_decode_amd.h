@@ -211,6 +211,20 @@ int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t
 int mla_decode_fwd(const mla_decode_args* args, void* stream);
 
 /*
+ * mla_decode_fwd without a workspace and without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The split partials and LSEs go to a static device
+ * array of MLA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until the process
+ * ends; args->workspace must be NULL and args->workspace_bytes 0.  A problem whose
+ * mla_workspace_bytes() exceeds MLA_NOALLOC_SCRATCH_BYTES is rejected with MLA_ERR_WORKSPACE
+ * before anything is launched.  Every call on one GPU uses that GPU's one array: calls that
+ * overlap on a GPU (other streams, other host threads) race, and the caller must order them.
+ * The same kernels and results as mla_decode_fwd.
+ */
+#define MLA_NOALLOC_SCRATCH_BYTES (160ll << 20)
+int mla_decode_fwd_noalloc(const mla_decode_args* args, void* stream);
+
+/*
  * Main split-KV kernel alone (the first half of mla_decode_fwd): sequences with a single
  * split are finished (out, lse); the partials of split sequences are left in `workspace`
  * for mla_combine_fwd.  Replaces the main TileLang kernel of mla_decode.py:78-192.

@@ -19,6 +19,7 @@ MLA_DEFAULT_SPLIT_OVERHEAD = 3  # pages; the default schedule's per-split overhe
 MLA_KV_NATIVE = 0
 MLA_KV_FP8_E4M3 = 1
 MLA_SPARSE_MAX_TOPK = 2048
+MLA_NOALLOC_SCRATCH_BYTES = 160 << 20  # the allocation-free decode's static scratch per GPU
 MLA_DIM_QK = 576
 MLA_DIM_V = 512
 MLA_PAGE_TOKENS = 64
@@ -33,6 +34,7 @@ EXPORTED = (
     "mla_get_metadata_host",
     "mla_workspace_bytes",
     "mla_decode_fwd",
+    "mla_decode_fwd_noalloc",
     "mla_splitkv_fwd",
     "mla_combine_fwd",
     "mla_merge_partials",
@@ -172,6 +174,8 @@ def load() -> ctypes.CDLL:
         lib.mla_workspace_bytes.restype = ctypes.c_int64
         lib.mla_decode_fwd.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]
         lib.mla_decode_fwd.restype = ctypes.c_int
+        lib.mla_decode_fwd_noalloc.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]
+        lib.mla_decode_fwd_noalloc.restype = ctypes.c_int
         lib.mla_splitkv_fwd.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]
         lib.mla_splitkv_fwd.restype = ctypes.c_int
         lib.mla_combine_fwd.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]

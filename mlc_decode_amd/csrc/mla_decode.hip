@@ -3003,6 +3003,50 @@ int mla_decode_fwd(const mla_decode_args* args, void* stream) {
   return launch_combine(kp, (const float*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
 }
 
+// The allocation-free decode's scratch: one array per GPU (each device that loads this code
+// object holds its own copy), addressed from the host only through the pointer that
+// hipGetSymbolAddress returns for that device.
+static __device__ __align__(256) uint8_t scratch[MLA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up once per device (with that device current).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("hipGetDevice failed: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MLA_ERR_UNSUPPORTED, "device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(MLA_ERR_HIP, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MLA_OK;
+}
+}  // namespace
+
+int mla_decode_fwd_noalloc(const mla_decode_args* args, void* stream) {
+  if (!args) return fail(MLA_ERR_INVALID, "args is NULL");
+  if (args->workspace != nullptr || args->workspace_bytes != 0)
+    return fail(MLA_ERR_INVALID, "mla_decode_fwd_noalloc takes no workspace (workspace NULL, workspace_bytes 0)");
+  const int64_t need = mla_workspace_bytes(args->batch, args->s_q, args->heads_q, args->num_parts);
+  if (need > MLA_NOALLOC_SCRATCH_BYTES)
+    return fail(MLA_ERR_WORKSPACE, "problem needs " + std::to_string(need) +
+                                       " workspace bytes, more than MLA_NOALLOC_SCRATCH_BYTES");
+  mla_decode_args a = *args;
+  const int rc = scratch_address(&a.workspace);
+  if (rc != MLA_OK) return rc;
+  a.workspace_bytes = MLA_NOALLOC_SCRATCH_BYTES;
+  return mla_decode_fwd(&a, stream);
+}
+
 int mla_splitkv_fwd(const mla_decode_args* args, void* stream) {
   int64_t need = 0;
   const int rc = validate(args, &need);

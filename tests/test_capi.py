@@ -209,6 +209,19 @@ def test_decode_rejects_bad_fp8_args(lib, changes, code, needle):
     assert needle in lib.mla_last_error()
 
 
+def test_decode_noalloc_rejects_workspace_and_oversize(lib):
+    # both checks run before any device call
+    a = _valid_args()
+    assert lib.mla_decode_fwd_noalloc(ctypes.byref(a), None) == 1
+    assert b"no workspace" in lib.mla_last_error()
+    a.workspace = None
+    a.workspace_bytes = 0
+    a.batch, a.heads_q, a.num_parts = 512, 128, 1024  # 1.1 GiB of partials
+    assert lib.mla_workspace_bytes(512, 1, 128, 1024) > _lib.MLA_NOALLOC_SCRATCH_BYTES
+    assert lib.mla_decode_fwd_noalloc(ctypes.byref(a), None) == 2
+    assert b"MLA_NOALLOC_SCRATCH_BYTES" in lib.mla_last_error()
+
+
 @pytest.mark.parametrize("w,v,code,needle", [
     (None, 1 << 20, 1, b"NULL"),
     (1 << 20, None, 1, b"NULL"),
