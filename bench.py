@@ -3,10 +3,13 @@
 A step is one decode call over the whole batch with inputs resident in HBM and the tile
 schedule computed beforehand (it is computed once per decode step and shared by every
 layer).  Prints ONE JSON line with the metric, the roofline of the dominant kernel (the
-split-KV main kernel, timed with HIP events on the launch stream) and the CPU oracle
-timed on the host cores as a baseline.
+split-KV main kernel, timed with HIP events on the launch stream), the same fraction for the
+whole call, the end-to-end time with the schedule included, the fraction of a measured
+stream peak, cold-cache times, and the CPU oracle timed on the host cores as a baseline.
 
     python bench.py [--steps K] [--warmup W] [--config C2] [--no-cpu-baseline]
+    python bench.py --stream-probe          # achievable HBM bandwidth of plain stream ops
+    python bench.py --all-configs [--record mla_best_configs_mi355x.json]
 """
 from __future__ import annotations
 
@@ -47,6 +50,10 @@ def parse():
     ap.add_argument("--kv-fp8", action="store_true",
                     help="measure the decode over the fp8 (e4m3) latent cache at every config (bf16 "
                          "queries); one JSON line per config")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="print the achievable HBM bandwidth of plain stream ops (fill, copy, add, "
+                         "sum over 1 GiB tensors) and exit")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timings")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain MIB-MiB device copy 3x (scale for FETCH/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -64,43 +71,74 @@ def cpu_model() -> str:
 
 
 def time_gpu(fn, steps, warmup, stream):
-    import torch
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        fn()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per call
+    from mlc_decode_amd.timing import time_gpu as _time_gpu
+    return _time_gpu(fn, steps, warmup, stream)
 
 
 def settle_clocks(fn, stream, seconds=0.25):
-    """Run ``fn`` back to back for about ``seconds`` before anything is timed.
+    from mlc_decode_amd.timing import settle_clocks as _settle
+    _settle(fn, stream, seconds)
 
-    A freshly idle GPU needs tens of milliseconds of load before its clocks settle: the first
-    200-call window measured cold reads ~10% slower than the next ones, whatever is timed.
-    This loop is untimed; the W warmup steps and the K timed steps follow it unchanged.
-    """
+
+FLUSH_BYTES = 1 << 30  # larger than the L2s and the 256 MB MALL together
+
+
+def time_cold(fn, reps, stream):
+    """Median ms of single calls, each after a 1 GiB fill that evicts the caches.  The fill
+    runs long enough for the host to queue the call behind it, so the GPU does not wait on
+    the host between the two events."""
+    import statistics
+
     import torch
+    junk = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda:0")
     fn()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    n = 1
-    while time.perf_counter() - t0 < seconds:
-        for _ in range(n):
-            fn()
+    times = []
+    for _ in range(reps):
+        junk.fill_(1)
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        fn()
+        e.record(stream)
         torch.cuda.synchronize()
-        n = min(n * 2, 256)
+        times.append(s.elapsed_time(e))
+    del junk
+    return statistics.median(times)
+
+
+def stream_probe(reps=20):
+    """Achievable HBM bandwidth of plain stream ops over 1 GiB tensors (GB/s of algorithmic
+    traffic, 10^9 bytes): the denominator of a measured-peak fraction, as the reference's
+    scripts/bandwidth_probe.py:52-71 measures its own device."""
+    import torch
+    n = FLUSH_BYTES // 2
+    x = torch.randn(n, dtype=torch.bfloat16, device="cuda:0")
+    y = torch.empty_like(x)
+    a = torch.randn(n, dtype=torch.bfloat16, device="cuda:0")
+    out = torch.empty_like(x)
+    nb = n * 2
+    cases = {
+        "fill_w": (lambda: y.fill_(1.0), nb),
+        "copy_rw": (lambda: y.copy_(x), 2 * nb),
+        "add_2r1w": (lambda: torch.add(x, a, out=out), 3 * nb),
+        "sum_r": (lambda: x.sum(dtype=torch.float32), nb),
+    }
+    res = {}
+    stream = torch.cuda.current_stream()
+    for name, (fn, traffic) in cases.items():
+        ms = time_gpu(fn, reps, 3, stream)
+        res[name] = round(traffic / (ms * 1e-3) / 1e9, 1)
+    del x, y, a, out
+    torch.cuda.empty_cache()
+    res["best"] = max(res.values())
+    return res
 
 
 FP8_TOKEN_BYTES = 512 + 64 * 2 + 4 * 4  # e4m3 latent codes, bf16 rope, four fp32 block scales
 
 
-def measure(cfg_name, steps, warmup, kv_fp8=False):
+def measure(cfg_name, steps, warmup, kv_fp8=False, cold=True):
     import dataclasses
 
     import torch
@@ -144,6 +182,15 @@ def measure(cfg_name, steps, warmup, kv_fp8=False):
                           steps, warmup, stream)
     ms_meta = time_gpu(lambda: get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=forced),
                        steps, warmup, stream)
+
+    def end_to_end():  # the schedule computed in the call, then the decode on it
+        sc, sp_ = get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=forced)
+        flash_mla_with_kvcache(inp.q, kv, inp.block_table, inp.cache_seqlens, 512,
+                               sc, sp_, softmax_scale=inp.sm_scale, causal=inp.causal,
+                               out=out, lse=lse)
+
+    ms_e2e = time_gpu(end_to_end, steps, warmup, stream)
+    ms_cold = None if not cold else time_cold(call, max(10, min(steps, 40)), stream)
     del keep
 
     nbytes = algorithmic_bytes(cpu_inp.cache_seqlens, B, s_q, H, 2)
@@ -156,8 +203,12 @@ def measure(cfg_name, steps, warmup, kv_fp8=False):
     gbs = nbytes / (ms_main * 1e-3) / 1e9
     tflops = flops / (ms_main * 1e-3) / 1e12
     n_splits = int(splits[-1].item())
+    # the same roofline over the whole call (main kernel, combine and the gap between them)
+    call_frac = (nbytes / (ms_call * 1e-3) / 1e9 / HBM_PEAK_GBS if bound == "hbm"
+                 else flops / (ms_call * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS)
     return dict(cfg=cfg, cpu_inp=cpu_inp, ms_call=ms_call, ms_main=ms_main, ms_combine=ms_combine,
-                ms_meta=ms_meta, nbytes=nbytes, flops=flops, bound=bound, gbs=gbs, tflops=tflops,
+                ms_meta=ms_meta, ms_e2e=ms_e2e, ms_cold=ms_cold, nbytes=nbytes, flops=flops,
+                bound=bound, gbs=gbs, tflops=tflops, call_frac=call_frac,
                 parts=int(sched.shape[0]), n_splits=n_splits)
 
 
@@ -350,6 +401,10 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if args.stream_probe:
+        print(json.dumps({"op": "stream_probe", "unit": "GB/s", "bytes_per_tensor": FLUSH_BYTES,
+                          **stream_probe()}), flush=True)
+        return
     if args.append:
         for name in ("C1", "C2", "C3", "C4", "C5"):
             print(json.dumps(measure_append(name, args.steps)), flush=True)
@@ -364,7 +419,7 @@ def main():
         return
     if args.kv_fp8:
         for name in ("C1", "C2", "C3", "C4", "C5"):
-            mm = measure(name, args.steps, args.warmup, kv_fp8=True)
+            mm = measure(name, args.steps, args.warmup, kv_fp8=True, cold=False)
             frac = (mm["gbs"] / HBM_PEAK_GBS) if mm["bound"] == "hbm" else (mm["tflops"] / MFMA_PEAK_TFLOPS)
             print(json.dumps({"op": "decode_fp8_cache", "config": name, "us_call": round(mm["ms_call"] * 1e3, 2),
                               "us_main": round(mm["ms_main"] * 1e3, 2),
@@ -382,7 +437,8 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    m = measure(args.config, args.steps, args.warmup)
+    probe = stream_probe()
+    m = measure(args.config, args.steps, args.warmup, cold=not args.no_cold)
     cfg = m["cfg"]
     if args.all_configs:
         from mlc_decode_amd import _lib
@@ -392,12 +448,15 @@ def main():
                   "peaks": {"hbm_gbs": HBM_PEAK_GBS, "mfma_bf16_tflops": MFMA_PEAK_TFLOPS},
                   "configs": {}}
         for name in ("C1", "C2", "C3", "C4", "C5"):
-            mm = m if name == args.config else measure(name, max(20, args.steps // 4), 5)
+            mm = m if name == args.config else measure(name, max(20, args.steps // 4), 5, cold=not args.no_cold)
             c = mm["cfg"]
             frac = (mm["gbs"] / HBM_PEAK_GBS) if mm["bound"] == "hbm" else (mm["tflops"] / MFMA_PEAK_TFLOPS)
             entry = {"us_call": round(mm["ms_call"] * 1e3, 2), "us_main": round(mm["ms_main"] * 1e3, 2),
                      "us_combine": round(mm["ms_combine"] * 1e3, 2),
                      "us_metadata": round(mm["ms_meta"] * 1e3, 2),
+                     "us_end_to_end": round(mm["ms_e2e"] * 1e3, 2),
+                     "us_call_cold": None if mm["ms_cold"] is None else round(mm["ms_cold"] * 1e3, 2),
+                     "call_frac": round(mm["call_frac"], 4),
                      "tbps": round(mm["gbs"] / 1e3, 3), "tflops": round(mm["tflops"], 1),
                      "bound": mm["bound"], "roofline_frac": round(frac, 4),
                      "parts": mm["parts"], "splits": mm["n_splits"]}
@@ -442,6 +501,13 @@ def main():
         "main_kernel_us": round(m["ms_main"] * 1e3, 3),
         "combine_us": round(m["ms_combine"] * 1e3, 3),
         "metadata_us": round(m["ms_meta"] * 1e3, 3),
+        "us_end_to_end_with_metadata": round(m["ms_e2e"] * 1e3, 3),
+        "us_call_cold": None if m["ms_cold"] is None else round(m["ms_cold"] * 1e3, 3),
+        "call_roofline_frac": round(m["call_frac"], 4),
+        "stream_probe_gbs": probe,
+        "frac_of_measured_peak": (round(m["gbs"] / probe["best"], 4) if m["bound"] == "hbm" else None),
+        "call_frac_of_measured_peak": (round(m["nbytes"] / (m["ms_call"] * 1e-3) / 1e9 / probe["best"], 4)
+                                       if m["bound"] == "hbm" else None),
         "roofline": {"bound": m["bound"], "achieved": round(achieved, 2), "peak": peak,
                      "unit": "GB/s" if m["bound"] == "hbm" else "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": traffic,
