@@ -195,10 +195,13 @@ int mla_get_metadata_host(const int32_t* cache_seqlens, int32_t batch, int32_t n
 
 /*
  * Workspace bytes mla_decode_fwd needs for this problem and part count: the per-split
- * log2-domain lse [slots, rows] fp32 (padded to 256 bytes), then the per-split
- * softmax-normalised partial outputs [slots, rows, 512] fp32, with slots = batch + num_parts.
- * (The reference's output_partial is in the input dtype, mla_decode.py:73-74; fp32 keeps
- * split outputs to one rounding, which bf16 needs to stay within 1e-2 for |out| in [2, 4).)
+ * log2-domain lse [slots, rows] fp32, then the scales [slots, rows, 4] fp32, then the
+ * per-split softmax-normalised partial outputs [slots, rows, 512] fp16 (each region padded to
+ * 256 bytes), with slots = batch + num_parts.  Chunk c (dims 128c .. 128c+127) of a partial row
+ * is stored times 2^e, e chosen from the chunk's amax so that it lands in [2^14, 2^15); the
+ * scale entry holds 2^-e.  Every value is then kept to 2^-11 of its chunk's amax.  (The
+ * reference's output_partial is unscaled in the input dtype, mla_decode.py:73-74; for bf16 a
+ * second bf16 rounding moves outputs in [2, 4) past 1e-2, which scaled fp16 does not.)
  */
 int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t num_parts);
 

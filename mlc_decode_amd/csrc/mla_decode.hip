@@ -82,8 +82,9 @@ struct KParams {
   int64_t o_sb, o_ss, o_sh;
   float* lse;
   float* ws_lse;    // [slots, rows] log2-domain lse of each split
-  float* ws_o;      // [slots, rows, 512] softmax-normalised partial outputs, fp32
-  int32_t part16;   // nonzero: ws_o holds the partials in the input dtype instead (mla_launch)
+  float* ws_scale;  // [slots, rows, 4] 2^-e of each 128-dim chunk of a partial row
+  uint16_t* ws_o;   // [slots, rows, 512] softmax-normalised partial outputs: fp16 times 2^e
+  int32_t part16;   // nonzero: ws_o holds unscaled partials in the input dtype (mla_launch)
   // fp8 latent cache only: kv_nope holds e4m3 codes (strides in bytes) and kv_scale the fp32
   // power-of-two scales, [page][128-dim block][token] with strides ks_sp, ks_sb (floats)
   const float* kv_scale;
@@ -166,6 +167,21 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
   else
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// Split partials in the decode workspace are fp16 with one power-of-two scale 2^e per (row,
+// 128-dim chunk), e chosen from the chunk's amax so that it lands in [2^14, 2^15): every value
+// is then held to 2^-11 of the chunk's amax, half the bytes of fp32 partials (bf16 partials
+// would move merged outputs in [2, 4) past the 1e-2 bar).  The workspace keeps 2^-e.
+__device__ __forceinline__ int part_exp(float amax) {
+  const int e = 15 - __builtin_amdgcn_frexp_expf(amax);  // amax = m * 2^E, m in [0.5, 1); 0 -> E = 0
+  return e < 127 ? e : 127;                               // amax < 2^-112: still below 2^15
+}
+__device__ __forceinline__ float exp2i(int e) {  // 2^e for e in [-126, 127]
+  return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
+}
+__device__ __forceinline__ float amax4(const f32x4 v) {
+  return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 }
 
 // acc + the sum of the eight 16-bit values packed in w (one v_dot2c_f32_{bf16,f16} per pair,
@@ -1226,13 +1242,19 @@ void mla_splitkv_kernel(KParams p) {
             *(i32x2*)d = i32x2{(int)pack2<DT>(a0[0], a0[1]), (int)pack2<DT>(a0[2], a0[3])};
             *(i32x2*)(d + 64) = i32x2{(int)pack2<DT>(a1[0], a1[1]), (int)pack2<DT>(a1[2], a1[3])};
           } else if (p.part16) {  // uniform: 16-bit partials (the reference's own format)
-            uint16_t* d = (uint16_t*)p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * cc;
+            uint16_t* d = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * cc;
             *(i32x2*)d = i32x2{(int)pack2<DT>(a0[0], a0[1]), (int)pack2<DT>(a0[2], a0[3])};
             *(i32x2*)(d + 64) = i32x2{(int)pack2<DT>(a1[0], a1[1]), (int)pack2<DT>(a1[2], a1[3])};
-          } else {  // the split's fp32 partial (rounded only once the splits are merged)
-            float* d = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * cc;
-            *(f32x4*)d = a0;
-            *(f32x4*)(d + 64) = a1;
+          } else {  // the split's scaled fp16 partial: chunk `wave` of row r spans lanes cc
+            float am = fmaxf(amax4(a0), amax4(a1));
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) am = fmaxf(am, __shfl_xor(am, off));
+            const int e = part_exp(am);
+            const f32x4 b0 = a0 * exp2i(e), b1 = a1 * exp2i(e);
+            uint16_t* d = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * cc;
+            *(i32x2*)d = i32x2{(int)pack2<MLA_DTYPE_F16>(b0[0], b0[1]), (int)pack2<MLA_DTYPE_F16>(b0[2], b0[3])};
+            *(i32x2*)(d + 64) = i32x2{(int)pack2<MLA_DTYPE_F16>(b1[0], b1[1]), (int)pack2<MLA_DTYPE_F16>(b1[2], b1[3])};
+            p.ws_scale[(slot * p.rows + row) * 4 + wave] = exp2i(-e);  // 16 lanes, one value
           }
         }
         if (wave == 0) {  // uniform: the four lane groups of a row store the same lse
@@ -1262,10 +1284,11 @@ void mla_splitkv_kernel(KParams p) {
       const int s = row / p.heads;
       const int h = row - s * p.heads;
       // A single-split sequence writes its output directly (rounded once to the input dtype);
-      // otherwise the split's partial goes to the workspace in fp32, so the output is still
-      // rounded only once, after the merge.  (The reference's split kernel rounds its partials
-      // to the input dtype, mla_decode.py:73-74,192; for bf16 a second rounding can move an
-      // output in [2, 4) by up to 2^-7, past the 1e-2 parity bar.)
+      // otherwise the split's partial goes to the workspace as scaled fp16 (each 128-dim chunk
+      // held to 2^-11 of its amax), so the merged output's error stays within the 1e-2 bar.
+      // (The reference's split kernel rounds its partials to the input dtype,
+      // mla_decode.py:73-74,192; for bf16 that second rounding can move an output in [2, 4) by
+      // up to 2^-7, past the bar.)
       const int64_t slot = slot0 + split;
       if (single) {  // uniform
         uint16_t* dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 4 * g;
@@ -1276,20 +1299,36 @@ void mla_splitkv_kernel(KParams p) {
           __builtin_amdgcn_sched_barrier(0);
         }
       } else if (p.part16) {  // uniform: 16-bit partials (the reference's own format)
-        uint16_t* dst = (uint16_t*)p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
+        uint16_t* dst = p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
 #pragma unroll
         for (int dt = 0; dt < kDimTiles; ++dt) {
           const f32x4 v = o[dt][ht] * inv;
           *(i32x2*)(dst + 16 * dt) = i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
           __builtin_amdgcn_sched_barrier(0);
         }
-      } else {
-        float* dst = p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
+      } else {  // scaled fp16: chunk c (tiles 8c .. 8c+7) of row li spans the four lane groups
+        float am[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dt = 0; dt < kDimTiles; ++dt) am[dt >> 3] = fmaxf(am[dt >> 3], amax4(o[dt][ht]));
+        int e[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float a = am[c] * inv;
+          a = fmaxf(a, __shfl_xor(a, 16));
+          a = fmaxf(a, __shfl_xor(a, 32));
+          e[c] = part_exp(a);
+        }
+        uint16_t* dst = p.ws_o + (slot * p.rows + row) * kDV + 4 * g;
 #pragma unroll
         for (int dt = 0; dt < kDimTiles; ++dt) {
-          *(f32x4*)(dst + 16 * dt) = o[dt][ht] * inv;
+          const f32x4 v = (o[dt][ht] * inv) * exp2i(e[dt >> 3]);
+          *(i32x2*)(dst + 16 * dt) =
+              i32x2{(int)pack2<MLA_DTYPE_F16>(v[0], v[1]), (int)pack2<MLA_DTYPE_F16>(v[2], v[3])};
           __builtin_amdgcn_sched_barrier(0);
         }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)  // the four lane groups store the same value (no divergence)
+          p.ws_scale[(slot * p.rows + row) * 4 + c] = exp2i(-e[c]);
       }
       if (single) {
         if (p.lse != nullptr) p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
@@ -1850,17 +1889,29 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
               i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
         }
       } else if (p.part16) {  // uniform
-        uint16_t* dst = (uint16_t*)p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * g_e;
+        uint16_t* dst = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * g_e;
 #pragma unroll
         for (int t = 0; t < WDT; ++t) {
           const f32x4 v = o[t][rt] * inv;
           *(i32x2*)(dst + 64 * (t & 1) + 16 * (t >> 1)) =
               i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
         }
-      } else {
-        float* dst = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * g_e;
+      } else {  // scaled fp16: the wave's chunk of row li spans the four lane groups
+        float am = 0.f;
 #pragma unroll
-        for (int t = 0; t < WDT; ++t) *(f32x4*)(dst + 64 * (t & 1) + 16 * (t >> 1)) = o[t][rt] * inv;
+        for (int t = 0; t < WDT; ++t) am = fmaxf(am, amax4(o[t][rt]));
+        am *= inv;
+        am = fmaxf(am, __shfl_xor(am, 16));
+        am = fmaxf(am, __shfl_xor(am, 32));
+        const int e = part_exp(am);
+        uint16_t* dst = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * g_e;
+#pragma unroll
+        for (int t = 0; t < WDT; ++t) {
+          const f32x4 v = (o[t][rt] * inv) * exp2i(e);
+          *(i32x2*)(dst + 64 * (t & 1) + 16 * (t >> 1)) =
+              i32x2{(int)pack2<MLA_DTYPE_F16>(v[0], v[1]), (int)pack2<MLA_DTYPE_F16>(v[2], v[3])};
+        }
+        p.ws_scale[(slot * p.rows + row) * 4 + wave] = exp2i(-e);  // four lane groups, one value
       }
     }
     // inv_sh is rewritten only after the next segment's barriers
@@ -1999,11 +2050,14 @@ __device__ __forceinline__ void load8(const uint16_t* src, float (&x)[8]) {
 // are exp2(lse_k - lse) with lse the log2-sum-exp2 over the row's n splits, staged through the
 // wave's 64-float LDS slot so every lane reads them; the partial rows are read four splits at a
 // time (independent loads).  Returns lse (log2; -inf when no split saw a key, acc then zero).
-// Shared by the combine and the fused absorb prologue, so both merge with the same arithmetic.
-template <int DT, typename PT>
-__device__ __forceinline__ float merge_splits_wave(const PT* __restrict__ ws_o, const float* __restrict__ ws_lse,
-                                                   int base, int n, int rows, int row, int lane, float* w_sh,
-                                                   float (&acc)[8]) {
+// SCALED: fp16 rows whose 128-dim chunk c carries the factor ws_scale[(slot, row) * 4 + c]
+// (lane l's chunk is l / 16), folded into the split weight.  The fused absorb prologue repeats
+// this arithmetic operation for operation.
+template <int DT, typename PT, bool SCALED>
+__device__ __forceinline__ float merge_splits_wave(const PT* __restrict__ ws_o, const float* __restrict__ ws_scale,
+                                                   const float* __restrict__ ws_lse, int base, int n, int rows,
+                                                   int row, int lane, float* w_sh, float (&acc)[8]) {
+  constexpr int LDT = SCALED ? MLA_DTYPE_F16 : DT;  // element type of the partial rows
   float mx = -INFINITY;
   for (int k = lane; k < n; k += 64) mx = fmaxf(mx, ws_lse[(int64_t)(base + k) * rows + row]);
 #pragma unroll
@@ -2019,6 +2073,8 @@ __device__ __forceinline__ float merge_splits_wave(const PT* __restrict__ ws_o, 
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
   const PT* src0 = ws_o + ((int64_t)base * rows + row) * kDV + lane * 8;
   const int64_t split_stride = (int64_t)rows * kDV;
+  const float* sc0 = SCALED ? ws_scale + ((int64_t)base * rows + row) * 4 + (lane >> 4) : nullptr;
+  const int64_t sc_stride = (int64_t)rows * 4;
   for (int k0 = 0; k0 < n; k0 += 64) {
     const int k = k0 + lane;
     float w = 0.f;
@@ -2028,20 +2084,23 @@ __device__ __forceinline__ float merge_splits_wave(const PT* __restrict__ ws_o, 
     const int kn = n - k0 < 64 ? n - k0 : 64;
     int kk = 0;
     for (; kk + 4 <= kn; kk += 4) {
-      float x[4][8];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) load8<DT>(src0 + (k0 + kk + u) * split_stride, x[u]);
+      float x[4][8], us[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const float wk = w_sh[kk + u];
+        load8<LDT>(src0 + (k0 + kk + u) * split_stride, x[u]);
+        us[u] = SCALED ? sc0[(k0 + kk + u) * sc_stride] : 1.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wk = w_sh[kk + u] * us[u];
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] += wk * x[u][j];
       }
     }
     for (; kk < kn; ++kk) {
       float x[8];
-      load8<DT>(src0 + (k0 + kk) * split_stride, x);
-      const float wk = w_sh[kk];
+      load8<LDT>(src0 + (k0 + kk) * split_stride, x);
+      const float wk = w_sh[kk] * (SCALED ? sc0[(k0 + kk) * sc_stride] : 1.f);
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] += wk * x[j];
     }
@@ -2051,8 +2110,9 @@ __device__ __forceinline__ float merge_splits_wave(const PT* __restrict__ ws_o, 
 }
 
 // One wave per (sequence, row).
-template <int DT, typename PT>
+template <int DT, typename PT, bool SCALED>
 __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__ ws_o,
+                                                          const float* __restrict__ ws_scale,
                                                           const float* __restrict__ ws_lse,
                                                           const int32_t* __restrict__ splits,
                                                           int rows, int heads, int s_q,
@@ -2070,7 +2130,8 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__
   const int n = splits[b + 1] - base;
   if (n < 1 || (n == 1 && !copy_single)) return;
   float acc[8];
-  const float lse2 = merge_splits_wave<DT>(ws_o, ws_lse, base, n, rows, row, lane, w_sh[wave], acc);
+  const float lse2 = merge_splits_wave<DT, PT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane,
+                                                       w_sh[wave], acc);
   const int s = row / heads;
   const int h = row - s * heads;
   uint16_t* dst = out + b * o_sb + s * o_ss + h * o_sh + lane * 8;
@@ -2103,8 +2164,9 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__
 constexpr int kVDim = 128;
 constexpr int kAbsRows = 16;
 struct AbsorbParams {
-  const float* ws_o;     // [slots, rows, 512] fp32 partials
-  const float* ws_lse;   // [slots, rows] log2
+  const uint16_t* ws_o;   // [slots, rows, 512] fp16 partials, chunk c times 2^e
+  const float* ws_scale;  // [slots, rows, 4] the chunks' 2^-e
+  const float* ws_lse;    // [slots, rows] log2
   const int32_t* splits;
   const uint16_t* out;   // single-split rows
   int64_t o_sb, o_ss, o_sh;
@@ -2121,7 +2183,7 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
   constexpr int R = RT / 4;        // rows merged by one wave
   constexpr int NT = 2;            // 16-column MFMA tiles per wave
   constexpr int KS = kDV / 32;     // MFMA k-steps
-  constexpr int kPF = 2;           // partial rows (fp32) per row loaded in one round trip
+  constexpr int kPF = 2;           // partial rows per row loaded in one round trip
   __shared__ __attribute__((aligned(16))) uint16_t a_sh[RT * kPitch];
   __shared__ float w_sh[RT][64];
   const int h = blockIdx.x;
@@ -2134,7 +2196,8 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
   const int64_t split_stride = (int64_t)a.rows * kDV;
   int n[R];
   const uint16_t* src1[R];  // single-split rows: the decode's output (input dtype)
-  const float* src[R];      // split rows: fp32 partials
+  const uint16_t* src[R];   // split rows: scaled fp16 partials
+  const float* scp[R];      // their scales (this lane's chunk, lane / 16)
   const float* lsep[R];
   int nmax = 0;
 #pragma unroll
@@ -2143,6 +2206,7 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
     n[i] = 0;
     src1[i] = a.out;
     src[i] = a.ws_o;
+    scp[i] = a.ws_scale;
     lsep[i] = a.ws_lse;
     if (m < a.m_rows) {
       const int b = m / a.s_q, s = m - b * a.s_q;
@@ -2153,25 +2217,31 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
         src1[i] = a.out + b * a.o_sb + s * a.o_ss + h * a.o_sh + lane * 8;
       } else {
         src[i] = a.ws_o + ((int64_t)base * a.rows + row) * kDV + lane * 8;
+        scp[i] = a.ws_scale + ((int64_t)base * a.rows + row) * 4 + (lane >> 4);
         lsep[i] = a.ws_lse + (int64_t)base * a.rows + row;
       }
     }
     nmax = n[i] > nmax ? n[i] : nmax;
   }
-  // the eight values of split u of row i owned by this lane, widened to fp32 (branches are
-  // wave-uniform: all lanes work on the same row)
-  auto load_row = [&](int u, int i, float (&xv)[8]) __attribute__((always_inline)) {
-    if (n[i] == 1) cvt8<DT>(*(const i32x4*)src1[i], xv);
-    else load8<DT>(src[i] + u * split_stride, xv);
+  // the eight values of split u of row i owned by this lane, widened to fp32, and their scale
+  // (1 for a single-split row; branches are wave-uniform: all lanes work on the same row)
+  auto load_row = [&](int u, int i, float (&xv)[8], float& us) __attribute__((always_inline)) {
+    if (n[i] == 1) {
+      cvt8<DT>(*(const i32x4*)src1[i], xv);
+      us = 1.f;
+    } else {
+      load8<MLA_DTYPE_F16>(src[i] + u * split_stride, xv);
+      us = scp[i][(int64_t)u * a.rows * 4];
+    }
   };
 
   // ---- 2. partial rows of the first kPF splits, and the lse of split `lane`, in one round trip
-  float x[kPF][R][8];
+  float x[kPF][R][8], us[kPF][R];
 #pragma unroll
   for (int u = 0; u < kPF; ++u)
 #pragma unroll
     for (int i = 0; i < R; ++i)
-      if (u < n[i]) load_row(u, i, x[u][i]);
+      if (u < n[i]) load_row(u, i, x[u][i], us[u][i]);
   float l0[R], lse2[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) l0[i] = (n[i] > 1 && lane < n[i]) ? lsep[i][(int64_t)lane * a.rows] : 0.f;
@@ -2224,14 +2294,14 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
         for (int u = 0; u < kPF; ++u)
 #pragma unroll
           for (int i = 0; i < R; ++i)
-            if (k0 + kb + u < n[i]) load_row(k0 + kb + u, i, x[u][i]);
+            if (k0 + kb + u < n[i]) load_row(k0 + kb + u, i, x[u][i], us[u][i]);
       }
 #pragma unroll
       for (int u = 0; u < kPF; ++u)
 #pragma unroll
         for (int i = 0; i < R; ++i)
           if (k0 + kb + u < n[i]) {
-            const float wk = w_sh[r0 + i][kb + u];
+            const float wk = w_sh[r0 + i][kb + u] * us[u][i];
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[i][j] += wk * x[u][i][j];
           }
@@ -2734,6 +2804,9 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 int64_t ws_lse_bytes(int64_t slots, int64_t rows) {
   return ((slots * rows * 4) + 255) / 256 * 256;
 }
+int64_t ws_scale_bytes(int64_t slots, int64_t rows) {
+  return ((slots * rows * 4 * 4) + 255) / 256 * 256;
+}
 
 template <int DT, int NW, int HT, int NS, bool WS, bool KV8 = false, bool SPARSE = false>
 hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) {
@@ -2886,7 +2959,8 @@ mla::KParams make_params(const mla_decode_args* a) {
   const int64_t rows = (int64_t)a->s_q * a->heads_q;
   const int64_t slots = (int64_t)a->batch + a->num_parts;
   k.ws_lse = (float*)a->workspace;
-  k.ws_o = (float*)((char*)a->workspace + ws_lse_bytes(slots, rows));
+  k.ws_scale = (float*)((char*)a->workspace + ws_lse_bytes(slots, rows));
+  k.ws_o = (uint16_t*)((char*)k.ws_scale + ws_scale_bytes(slots, rows));
   k.batch = a->batch;
   k.s_q = a->s_q;
   k.heads = a->heads_q;
@@ -2897,18 +2971,18 @@ mla::KParams make_params(const mla_decode_args* a) {
   return k;
 }
 
-// Partials are fp32 rows (the decode workspace, the caller's rows of mla_merge_partials) or
-// the 16-bit rows of mla_launch (PT = uint16_t).
-template <typename PT>
+// Partials are the decode workspace's scaled fp16 rows (SCALED), the caller's fp32 rows of
+// mla_merge_partials, or the unscaled 16-bit rows of mla_launch (PT = uint16_t).
+template <typename PT, bool SCALED = false>
 int launch_combine(const mla::KParams& k, const PT* part_o, int dtype, int copy_single, hipStream_t st) {
   dim3 grid(k.batch, (k.rows + 3) / 4);
   if (dtype == MLA_DTYPE_BF16)
-    hipLaunchKernelGGL((mla::mla_combine_kernel<MLA_DTYPE_BF16, PT>), grid, dim3(256), 0, st, part_o,
-                       k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
+    hipLaunchKernelGGL((mla::mla_combine_kernel<MLA_DTYPE_BF16, PT, SCALED>), grid, dim3(256), 0, st, part_o,
+                       k.ws_scale, k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
                        k.lse, copy_single);
   else
-    hipLaunchKernelGGL((mla::mla_combine_kernel<MLA_DTYPE_F16, PT>), grid, dim3(256), 0, st, part_o,
-                       k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
+    hipLaunchKernelGGL((mla::mla_combine_kernel<MLA_DTYPE_F16, PT, SCALED>), grid, dim3(256), 0, st, part_o,
+                       k.ws_scale, k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
                        k.lse, copy_single);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
@@ -2993,14 +3067,14 @@ int64_t mla_workspace_bytes(int32_t batch, int32_t s_q, int32_t heads_q, int32_t
   if (batch < 1 || s_q < 1 || heads_q < 1 || num_parts < 1) return 0;
   const int64_t rows = (int64_t)s_q * heads_q;
   const int64_t slots = (int64_t)batch + num_parts;
-  return ws_lse_bytes(slots, rows) + slots * rows * mla::kDV * 4;
+  return ws_lse_bytes(slots, rows) + ws_scale_bytes(slots, rows) + slots * rows * mla::kDV * 2;
 }
 
 int mla_decode_fwd(const mla_decode_args* args, void* stream) {
   const int rc = mla_splitkv_fwd(args, stream);
   if (rc != MLA_OK) return rc;
   const mla::KParams kp = make_params(args);
-  return launch_combine(kp, (const float*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
+  return launch_combine<uint16_t, true>(kp, kp.ws_o, args->dtype, 0, (hipStream_t)stream);
 }
 
 // The allocation-free decode's scratch: one array per GPU (each device that loads this code
@@ -3067,7 +3141,7 @@ int mla_combine_fwd(const mla_decode_args* args, void* stream) {
   const int rc = validate(args, &need);
   if (rc != MLA_OK) return rc;
   const mla::KParams kp = make_params(args);
-  return launch_combine(kp, (const float*)kp.ws_o, args->dtype, 0, (hipStream_t)stream);
+  return launch_combine<uint16_t, true>(kp, kp.ws_o, args->dtype, 0, (hipStream_t)stream);
 }
 
 int mla_combine_absorb(const mla_decode_args* args, const void* w_uv_blk, void* v, void* stream) {
@@ -3080,6 +3154,7 @@ int mla_combine_absorb(const mla_decode_args* args, const void* w_uv_blk, void* 
   const mla::KParams kp = make_params(args);
   mla::AbsorbParams a{};
   a.ws_o = kp.ws_o;
+  a.ws_scale = kp.ws_scale;
   a.ws_lse = kp.ws_lse;
   a.splits = kp.splits;
   a.out = kp.out;
@@ -3192,7 +3267,7 @@ void mla_launch(const void* Q, const void* Qpe, const void* KV, const void* Kpe,
   k.lse = nullptr;
   // lse_bytes + 16 * 512 * 2 * ns <= 18432 ns bytes for every ns >= 1
   k.ws_lse = (float*)partial;
-  k.ws_o = (float*)((char*)partial + lse_bytes);
+  k.ws_o = (uint16_t*)((char*)partial + lse_bytes);
   k.part16 = 1;
   k.batch = 1;
   k.s_q = 1;
@@ -3209,7 +3284,7 @@ void mla_launch(const void* Q, const void* Qpe, const void* KV, const void* Kpe,
     fail(MLA_ERR_HIP, std::string("mla_launch: launch failed: ") + hipGetErrorString(e));
     return;
   }
-  launch_combine(k, (const uint16_t*)k.ws_o, MLA_DTYPE_F16, 0, st);
+  launch_combine(k, (const uint16_t*)k.ws_o, MLA_DTYPE_F16, 0, st);  // unscaled 16-bit rows
 }
 
 int mla_kv_append(const mla_kv_append_args* a, void* stream) {

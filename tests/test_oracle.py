@@ -375,11 +375,27 @@ def test_check_cli_reference_equals_oracle():
         assert torch.allclose(got, want, atol=1e-6, rtol=1e-5)
 
 
+def _scaled_f16(po):
+    """Split partials as the decode workspace holds them: fp16 times 2^e per 128-dim chunk of a
+    row, e = 15 - E for chunk amax = m 2^E, m in [0.5, 1) (the chunk lands in [2^14, 2^15)),
+    then multiplied back by 2^-e as the combine does."""
+    out = po.clone()
+    for c in range(4):
+        ch = po[..., 128 * c:128 * (c + 1)]
+        amax = ch.abs().amax(-1, keepdim=True)
+        _, E = torch.frexp(amax)
+        e = (15 - E).clamp(max=127).to(po.dtype)
+        out[..., 128 * c:128 * (c + 1)] = (ch * torch.exp2(e)).to(torch.float16).to(po.dtype) * torch.exp2(-e)
+    return out
+
+
 def test_bf16_partials_break_the_bar():
-    """Why the decode keeps split partials in fp32.  Outputs in [2, 4) (latent dims drawn in
-    that band) merged from 4 splits: with fp32 partials the error against the fp32 oracle is
-    the output's own bf16 rounding (<= 2^-7 = 0.0078); with partials rounded to bf16 before the
-    merge (the reference's partial format, mla_decode.py:73-74) it passes 1e-2."""
+    """Why the decode does not keep split partials in bf16.  Outputs in [2, 4) (latent dims
+    drawn in that band) merged from 4 splits: with fp32 partials the error against the fp32
+    oracle is the output's own bf16 rounding (<= 2^-7 = 0.0078); with partials rounded to bf16
+    before the merge (the reference's partial format, mla_decode.py:73-74) it passes 1e-2; with
+    the decode's scaled fp16 partials (2^-11 of each 128-dim chunk's amax, here <= 2^-10) it
+    stays within 2^-7 + 2^-10."""
     g = torch.Generator().manual_seed(3)
     H, L, S = 16, 1024, 4
     q = (torch.randn(H, 576, generator=g) * 3).to(torch.bfloat16).double()
@@ -396,9 +412,29 @@ def test_bf16_partials_break_the_bar():
         lses.append(torch.logsumexp(s[:, sl], -1))
     part_o, part_l = torch.stack(parts), torch.stack(lses)
     errs = {}
-    for name, po in (("fp32", part_o.float()), ("bf16", part_o.to(torch.bfloat16).float())):
+    for name, po in (("fp32", part_o.float()), ("bf16", part_o.to(torch.bfloat16).float()),
+                     ("f16s", _scaled_f16(part_o.float()))):
         out, lse = R.combine(po, part_l.float())
         assert (lse.double() - torch.logsumexp(s, -1)).abs().max() < 1e-4
         errs[name] = (out.to(torch.bfloat16).double() - ref).abs().max().item()
     assert errs["fp32"] <= 2 ** -7 + 1e-6
     assert errs["bf16"] > 1e-2
+    assert errs["f16s"] <= 2 ** -7 + 2 ** -10 + 1e-6 < 1e-2
+
+
+def test_scaled_f16_partials_error_bound():
+    """The scaled fp16 partial format on chunks of very different magnitudes, signs, zeros and
+    extreme exponents: every value comes back within 2^-11 of its chunk's amax."""
+    g = torch.Generator().manual_seed(4)
+    po = torch.randn(3, 5, 512, generator=g, dtype=torch.float64)
+    po[0, 0, :128] *= 1e-30          # tiny chunk
+    po[0, 1, 128:256] *= 3e4         # large chunk
+    po[1, 2, 256:384] = 0.0          # all-zero chunk
+    po[2, 3, 384:] = -7.5            # constant negative chunk
+    po[2, 4, :] *= 2.0 ** -100
+    back = _scaled_f16(po.float()).double()
+    for c in range(4):
+        ch = po[..., 128 * c:128 * (c + 1)].float().double()
+        amax = ch.abs().amax(-1, keepdim=True)
+        err = (back[..., 128 * c:128 * (c + 1)] - ch).abs()
+        assert torch.all(err <= amax * 2.0 ** -11)
