@@ -245,6 +245,19 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
       : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
       : "memory", "m0");
 }
+// The same copy with the LDS destination given as an SGPR plus an immediate (one SALU op,
+// written straight into M0): the wide kernel's stage loads, which step the global address in
+// the per-lane offset instead of the SGPR base (the instruction's immediate offset would move
+// the LDS address too), so a load costs one scalar instruction.
+template <int LDS_OFF>
+__device__ __forceinline__ void dma16_m0(uint64_t sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile(
+      "s_add_u32 m0, %2, %3\n\t"
+      "global_load_lds_dwordx4 %0, %1 nt"
+      :
+      : "v"(voff), "s"(sbase), "s"(lds_base), "i"(LDS_OFF)
+      : "memory", "m0", "scc");
+}
 // The same copy from a per-lane 64-bit address (the sparse path: every token row has its own
 // page).
 __device__ __forceinline__ void dma16_lane(const void* addr, uint32_t lds_addr) {
@@ -1502,44 +1515,80 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     // be spread between MFMAs (in a burst they hold the wave for ~900 cycles behind the CU's
     // load path; spread, ~10 each).  Rows past the sequence end re-read its last row.
     struct StageIssue {
-      const char* nb;   // latent row base of the stage (bytes)
-      const char* rb;   // rope row base
+      uint64_t nb, rb;  // latent and rope row bases of the stage (bytes, uniform)
       uint32_t on, orp; // per-lane byte offsets
-      uint32_t lat_dst, rope_dst;
+      uint32_t lat_dst, rope_dst;  // LDS destinations (uniform)
     };
+    // A stage past the segment (the loop's last iterations) is still issued, to the ring slot
+    // that is free at that point, with every lane reading the segment's last row: the loads
+    // cost a cache line, and the wait counts stay the same in every iteration.
     auto prepare = [&](int k) __attribute__((always_inline)) {
-      const int st = st_begin + k;
+      const bool real = k < nst;
+      const int st = st_begin + (real ? k : nst - 1);
       StageIssue si;
       const int tok = (st & 1) * kStageTok;
+      const char* nb;
+      const char* rb;
       if (paged) {
         const int pidx = st >> 1;
         if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
         const uint32_t pg = (uint32_t)__builtin_amdgcn_readlane(bt_lane, pidx - pbase);
-        si.nb = (const char*)p.kv_nope + ((uint64_t)pg * (uint32_t)p.kv_sp + (uint32_t)(tok * kv_st)) * 2;
-        si.rb = (const char*)p.kv_rope + ((uint64_t)pg * (uint32_t)p.kr_sp + (uint32_t)(tok * kr_st)) * 2;
+        nb = (const char*)p.kv_nope + ((uint64_t)pg * (uint32_t)p.kv_sp + (uint32_t)(tok * kv_st)) * 2;
+        rb = (const char*)p.kv_rope + ((uint64_t)pg * (uint32_t)p.kr_sp + (uint32_t)(tok * kr_st)) * 2;
       } else {
-        si.nb = (const char*)(p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st * kStageTok * kv_st));
-        si.rb = (const char*)(p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st));
+        nb = (const char*)(p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st * kStageTok * kv_st));
+        rb = (const char*)(p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st));
       }
+      const auto uni64 = [](const char* q) {
+        const uint64_t v = (uint64_t)(uintptr_t)q;
+        return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32) |
+               (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+      };
+      si.nb = uni64(nb);
+      si.rb = uni64(rb);
       const int left = L - st * kStageTok;
       const int last_row = (left < kStageTok ? left : kStageTok) - 1;
       int row = 8 * wave + (lane >> 3);
-      row = row < last_row ? row : last_row;
-      const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((wave & 1) << 3) | (lane >> 3))) << 4);
+      row = row < last_row && real ? row : last_row;
+      const uint32_t cl = real ? (uint32_t)(((lane & 7) ^ stage_swz(((wave & 1) << 3) | (lane >> 3))) << 4) : 0u;
       si.on = (uint32_t)(row * kv_st) * 2 + cl;
       si.orp = (uint32_t)(row * kr_st) * 2 + cl;
-      si.lat_dst = (uint32_t)(uintptr_t)(lat + (k % kWideLat) * kLatStageBytes + wave * 8 * 1024);
-      si.rope_dst = (uint32_t)(uintptr_t)(rope + (k % kWideRope) * kRopeStageBytes + wave * 1024);
+      si.lat_dst = (uint32_t)__builtin_amdgcn_readfirstlane(
+          (int)(uint32_t)(uintptr_t)(lat + (k % kWideLat) * kLatStageBytes + wave * 8 * 1024));
+      si.rope_dst = (uint32_t)__builtin_amdgcn_readfirstlane(
+          (int)(uint32_t)(uintptr_t)(rope + (k % kWideRope) * kRopeStageBytes + wave * 1024));
       return si;
     };
-    auto issue_one = [&](const StageIssue& si, int j) __attribute__((always_inline)) {
-      if (j < 8) dma16(si.nb + 128 * j, si.on, si.lat_dst + j * 1024);
-      else dma16(si.rb, si.orp, si.rope_dst);
+    auto issue_one = [&](const StageIssue& si, auto jtag) __attribute__((always_inline)) {
+      constexpr int j = decltype(jtag)::value;
+      if constexpr (j < 8) dma16_m0<j * 1024>(si.nb, si.on + 128 * j, si.lat_dst);
+      else dma16_m0<0>(si.rb, si.orp, si.rope_dst);
+    };
+    // load j (a constant once the loops around the call are unrolled)
+    auto issue_j = [&](const StageIssue& si, int j) __attribute__((always_inline)) {
+      switch (j) {
+        case 0: issue_one(si, std::integral_constant<int, 0>{}); break;
+        case 1: issue_one(si, std::integral_constant<int, 1>{}); break;
+        case 2: issue_one(si, std::integral_constant<int, 2>{}); break;
+        case 3: issue_one(si, std::integral_constant<int, 3>{}); break;
+        case 4: issue_one(si, std::integral_constant<int, 4>{}); break;
+        case 5: issue_one(si, std::integral_constant<int, 5>{}); break;
+        case 6: issue_one(si, std::integral_constant<int, 6>{}); break;
+        case 7: issue_one(si, std::integral_constant<int, 7>{}); break;
+        default: issue_one(si, std::integral_constant<int, 8>{}); break;
+      }
     };
     auto issue = [&](int k) __attribute__((always_inline)) {  // all nine at once
       const StageIssue si = prepare(k);
-#pragma unroll
-      for (int j = 0; j < 9; ++j) issue_one(si, j);
+      issue_one(si, std::integral_constant<int, 0>{});
+      issue_one(si, std::integral_constant<int, 1>{});
+      issue_one(si, std::integral_constant<int, 2>{});
+      issue_one(si, std::integral_constant<int, 3>{});
+      issue_one(si, std::integral_constant<int, 4>{});
+      issue_one(si, std::integral_constant<int, 5>{});
+      issue_one(si, std::integral_constant<int, 6>{});
+      issue_one(si, std::integral_constant<int, 7>{});
+      issue_one(si, std::integral_constant<int, 8>{});
     };
 
     // One pass over the segment's stages; returns true (uniformly) when a first-stage-reference
@@ -1593,7 +1642,9 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
       // S^T = K Q^T of stage k over 576 dims: two 16-token tiles x HT row tiles, fragment
       // n = 2*kk + tt, DK fragments in flight.  Loads 0..3 of `si` go out after steps 4, 12, 20
       // and 28; with `vt`, the V^T fragments of stage k-1 are read during the last 8 steps.
-      auto qk = [&](int k, f32x4 (&acc)[HT][2], const LaneOffsets& lo, const StageIssue& si, bool do_issue,
+      // issue_tag: std::true_type to issue loads 0..3 of `si` between the MFMAs (the stage loop),
+      // std::false_type for the peeled first iteration, which has no stage to issue
+      auto qk = [&](int k, f32x4 (&acc)[HT][2], const LaneOffsets& lo, const StageIssue& si, auto issue_tag,
                     bool vt, i32x4 (&va)[WDT]) __attribute__((always_inline)) {
         const uint8_t LDS_AS* lb = lat + (k % kWideLat) * kLatStageBytes;
         const uint8_t LDS_AS* rbs = rope + (k % kWideRope) * kRopeStageBytes;
@@ -1624,7 +1675,9 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
             else
               mfma_qk<DT>(acc[ht][n & 1], a, qf[ht][n >> 1]);
           }
-          if ((n & 7) == 4 && do_issue) issue_one(si, n >> 3);  // loads 0..3
+          if constexpr (decltype(issue_tag)::value) {
+            if ((n & 7) == 4) issue_j(si, n >> 3);  // loads 0..3
+          }
           if (n >= 2 * kKSteps - WDT && vt) va[n - (2 * kKSteps - WDT)] = v_frag(vb, n - (2 * kKSteps - WDT));
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -1689,7 +1742,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
       // (8 MFMAs), then computes two P elements; the slicing is fixed in source order (one
       // scheduling barrier per step), which also bounds how many operands are live at once.
       auto pv_softmax = [&](int kp, const f32x4 (&acc)[HT][2], const i32x4 (&va)[WDT],
-                            const StageIssue& si, bool do_issue) __attribute__((always_inline)) {
+                            const StageIssue& si) __attribute__((always_inline)) {
         const uint8_t LDS_AS* pp = ptb + (kp & 1) * kPBytes + lane * 16;
         asm volatile("" : "+v"(pp));
         uint8_t LDS_AS* pw = ptb + ((kp + 1) & 1) * kPBytes + lane * 16;
@@ -1731,7 +1784,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
           // loads 4..8 after steps (2i + 1) * RT / 10
 #pragma unroll
           for (int i = 0; i < 5; ++i)
-            if (rt == (2 * i + 1) * RT / 10 && do_issue) issue_one(si, 4 + i);
+            if (rt == (2 * i + 1) * RT / 10) issue_j(si, 4 + i);
           __builtin_amdgcn_sched_barrier(0);
           b_last = bcur;
         }
@@ -1752,7 +1805,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         const LaneOffsets lo = lane_offsets(ln0);
         f32x4 acc[HT][2];
         i32x4 va_unused[WDT];
-        qk(0, acc, lo, StageIssue{}, false, false, va_unused);
+        qk(0, acc, lo, StageIssue{}, std::false_type{}, false, va_unused);
         float lmx[HT];
         mask_max(0, acc, lmx);
         if constexpr (MODE == kPassRowMax) {
@@ -1784,16 +1837,14 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
           flag_word = over_sh[(k - 1) & 3];
           if (k >= 3 && wave == 0) over_sh[(k - 2) & 3] = 0;
         }
-        const bool do_issue = k + 2 < nst;  // uniform
-        StageIssue si{};
-        if (do_issue) si = prepare(k + 2);
+        const StageIssue si = prepare(k + 2);  // past the segment: dummy loads (see prepare)
         int ln = lane;
         asm volatile("" : "+v"(ln));  // opaque per iteration: the offsets stay inside the loop
         const LaneOffsets lo = lane_offsets(ln);
         f32x4 acc[HT][2];
         i32x4 va[WDT];
         if (has_qk) {
-          qk(k, acc, lo, si, do_issue, kPV, va);
+          qk(k, acc, lo, si, std::true_type{}, kPV, va);
         } else {
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht)
@@ -1816,10 +1867,8 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         if constexpr (MODE == kPassRowMax) {
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) m_ref[ht] = fmaxf(m_ref[ht], lmx[ht]);
-          if (do_issue) {
 #pragma unroll
-            for (int j = 4; j < 9; ++j) issue_one(si, j);
-          }
+          for (int j = 4; j < 9; ++j) issue_j(si, j);
           continue;
         }
         bool over = false;
@@ -1827,7 +1876,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
         }
-        if constexpr (kPV) pv_softmax(k - 1, acc, va, si, do_issue);
+        if constexpr (kPV) pv_softmax(k - 1, acc, va, si);
         if constexpr (MODE == kPassFirstStageRef) {
           if (__builtin_amdgcn_ballot_w64(over) != 0) over_sh[k & 3] = 1;  // uniform branch
         }
