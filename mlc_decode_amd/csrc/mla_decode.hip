@@ -96,6 +96,9 @@ struct KParams {
   int64_t pool_tokens;
   int32_t batch, s_q, heads, rows, causal, num_parts;
   float scale_log2;  // sm_scale * log2(e)
+  // wide kernel, 1-D grid: the xcd_hb head blocks of a part are consecutive workgroups on one
+  // XCD (0: a (part, head block) grid)
+  int32_t xcd_hb;
 };
 
 // ---------------------------------------------------------------------------------------
@@ -248,12 +251,14 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
 // The same copy with the LDS destination given as an SGPR plus an immediate (one SALU op,
 // written straight into M0): the wide kernel's stage loads, which step the global address in
 // the per-lane offset instead of the SGPR base (the instruction's immediate offset would move
-// the LDS address too), so a load costs one scalar instruction.
+// the LDS address too), so a load costs one scalar instruction.  Without the non-temporal
+// hint: workgroups that stream the same pages (the head blocks of a part, neighbouring splits)
+// find them in L2 (measured: 12% fewer fetched bytes at 256 rows, 9% faster at 64 rows).
 template <int LDS_OFF>
 __device__ __forceinline__ void dma16_m0(uint64_t sbase, uint32_t voff, uint32_t lds_base) {
   asm volatile(
       "s_add_u32 m0, %2, %3\n\t"
-      "global_load_lds_dwordx4 %0, %1 nt"
+      "global_load_lds_dwordx4 %0, %1"
       :
       : "v"(voff), "s"(sbase), "s"(lds_base), "i"(LDS_OFF)
       : "memory", "m0", "scc");
@@ -1414,8 +1419,20 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   uint8_t LDS_AS* const rope = (uint8_t LDS_AS*)rope_raw;
   uint8_t LDS_AS* const ptb = (uint8_t LDS_AS*)pt_raw;
 
-  const int part = blockIdx.x;
-  const int hb = blockIdx.y;
+  // Workgroups are handed to the 8 XCDs round-robin by linear id, each XCD starting its own
+  // in order.  With several head blocks, the grid is 1-D and id L maps to slot L / 8 on XCD
+  // L % 8, slot -> (part, head block) with the head blocks of a part in consecutive slots: the
+  // workgroups that stream the same pages run side by side on one XCD and share its L2.
+  int part, hb;
+  if (p.xcd_hb > 1) {
+    const int L = blockIdx.x;
+    const int slot = L >> 3;
+    hb = slot % p.xcd_hb;
+    part = (slot / p.xcd_hb) * 8 + (L & 7);
+  } else {
+    part = blockIdx.x;
+    hb = blockIdx.y;
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
@@ -1472,6 +1489,18 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
     const int nst = st_end > st_begin ? st_end - st_begin : 0;
 
+    int pbase = 0, bt_lane = 0;
+
+    // page ids pbase .. pbase + 63 of the sequence, one per lane, clamped into the pool
+    auto load_page_ids = [&](int first) __attribute__((always_inline)) {
+      pbase = first;
+      if (paged) {
+        const int last = np > 0 ? np - 1 : 0;
+        const int pi = pbase + lane < last ? pbase + lane : last;
+        const int v = p.block_table[(int64_t)b * p.bt_stride + pi];
+        bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
+      }
+    };
     // ---- query fragments of this wave's rows (B operand of S^T = K Q^T), resident for the
     // segment; rows past the end re-load the last row (their results are never written)
     i32x4 qf[HT][kKSteps];
@@ -1497,20 +1526,9 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     // row sums of this wave's QK rows: l_part over P as rounded for PV (normalises the
     // output), l_exact over the fp32 P (gives the lse)
     float m_ref[HT], l_part[HT], l_exact[HT];
-    int pbase = 0, bt_lane = 0;
-
-    auto load_page_ids = [&](int first) __attribute__((always_inline)) {
-      pbase = first;
-      if (paged) {
-        const int last = np > 0 ? np - 1 : 0;
-        const int pi = pbase + lane < last ? pbase + lane : last;
-        const int v = p.block_table[(int64_t)b * p.bt_stride + pi];
-        bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
-      }
-    };
     // The loads of one stage: wave w fetches row group w, 8 latent blocks and 1 rope block (one
     // global_load_lds_dwordx4 each, eight lanes per 128-byte line).  `prepare` does the scalar
-    // work once (page lookup, 32 x 32 -> 64-bit page offset: page strides are below 2^31
+    // work once (page lookup, 32 x 32 -> 64-bit page offset: page strides are below 2^32
     // elements, checked by the host); `issue_one(si, j)` issues load j, so the nine loads can
     // be spread between MFMAs (in a burst they hold the wave for ~900 cycles behind the CU's
     // load path; spread, ~10 each).  Rows past the sequence end re-read its last row.
@@ -2878,7 +2896,13 @@ bool wide_enabled() {
 
 template <int DT, int HT>
 hipError_t launch_wide(const mla::KParams& kp, int head_blocks, hipStream_t st) {
-  hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT>), dim3(kp.num_parts, head_blocks), dim3(256), 0, st, kp);
+  if (head_blocks > 1 && kp.num_parts % 8 == 0) {  // head blocks of a part side by side on one XCD
+    mla::KParams k = kp;
+    k.xcd_hb = head_blocks;
+    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT>), dim3(kp.num_parts * head_blocks), dim3(256), 0, st, k);
+  } else {
+    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT>), dim3(kp.num_parts, head_blocks), dim3(256), 0, st, kp);
+  }
   return hipGetLastError();
 }
 
