@@ -54,6 +54,8 @@ def parse():
                     help="print the achievable HBM bandwidth of plain stream ops (fill, copy, add, "
                          "sum over 1 GiB tensors) and exit")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timings")
+    ap.add_argument("--no-probe", action="store_true",
+                    help="skip the stream probe (profiling runs: keeps its copies out of the trace)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain MIB-MiB device copy 3x (scale for FETCH/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -437,7 +439,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    probe = stream_probe()
+    probe = None if args.no_probe else stream_probe()
     m = measure(args.config, args.steps, args.warmup, cold=not args.no_cold)
     cfg = m["cfg"]
     if args.all_configs:
@@ -505,9 +507,9 @@ def main():
         "us_call_cold": None if m["ms_cold"] is None else round(m["ms_cold"] * 1e3, 3),
         "call_roofline_frac": round(m["call_frac"], 4),
         "stream_probe_gbs": probe,
-        "frac_of_measured_peak": (round(m["gbs"] / probe["best"], 4) if m["bound"] == "hbm" else None),
+        "frac_of_measured_peak": (round(m["gbs"] / probe["best"], 4) if m["bound"] == "hbm" and probe else None),
         "call_frac_of_measured_peak": (round(m["nbytes"] / (m["ms_call"] * 1e-3) / 1e9 / probe["best"], 4)
-                                       if m["bound"] == "hbm" else None),
+                                       if m["bound"] == "hbm" and probe else None),
         "roofline": {"bound": m["bound"], "achieved": round(achieved, 2), "peak": peak,
                      "unit": "GB/s" if m["bound"] == "hbm" else "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": traffic,
