@@ -2082,8 +2082,8 @@ __global__ __launch_bounds__(256) void mla_kv_append_kernel(AppendParams a) {
 // ---------------------------------------------------------------------------------------
 // combine: LSE-weighted merge of the splits of each (sequence, row)
 // ---------------------------------------------------------------------------------------
-// Eight consecutive partial values of one row, widened to fp32: the fp32 rows of the decode
-// workspace and of mla_merge_partials, or the 16-bit rows of mla_launch.
+// Eight consecutive partial values of one row, widened to fp32: the fp32 rows of
+// mla_merge_partials, or the 16-bit rows of the decode workspace and of mla_launch.
 template <int DT>
 __device__ __forceinline__ void load8(const float* src, float (&x)[8]) {
   const f32x4 a = *(const f32x4*)src;

@@ -103,9 +103,9 @@ def test_host_schedule_matches_oracle(seed):
 def test_workspace_bytes(lib):
     n = lib.mla_workspace_bytes(64, 1, 128, 128)
     slots, rows = 64 + 128, 128
-    # fp32 lse per (slot, row) padded to 256 bytes, then fp32 partial rows of 512
     pad = lambda x: -(-x // 256) * 256  # noqa: E731
-    # lse fp32, one scale per 128-dim chunk (fp32), fp16 partial rows
+    # fp32 lse per (slot, row), one fp32 scale per 128-dim chunk (each padded to 256 bytes),
+    # then fp16 partial rows of 512
     assert n == pad(slots * rows * 4) + pad(slots * rows * 16) + slots * rows * 512 * 2
     assert lib.mla_workspace_bytes(0, 1, 16, 4) == 0
 
