@@ -96,8 +96,9 @@ struct KParams {
   int64_t pool_tokens;
   int32_t batch, s_q, heads, rows, causal, num_parts;
   float scale_log2;  // sm_scale * log2(e)
-  // wide kernel, 1-D grid: the xcd_hb head blocks of a part are consecutive workgroups on one
-  // XCD (0: a (part, head block) grid)
+  // wide kernel, 1-D grid of num_parts * xcd_hb workgroups (a multiple of 8): XCD x runs a
+  // contiguous block of parts, the xcd_hb head blocks of a part in consecutive slots
+  // (0: a (part, head block) grid)
   int32_t xcd_hb;
 };
 
@@ -1420,15 +1421,17 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   uint8_t LDS_AS* const ptb = (uint8_t LDS_AS*)pt_raw;
 
   // Workgroups are handed to the 8 XCDs round-robin by linear id, each XCD starting its own
-  // in order.  With several head blocks, the grid is 1-D and id L maps to slot L / 8 on XCD
-  // L % 8, slot -> (part, head block) with the head blocks of a part in consecutive slots: the
-  // workgroups that stream the same pages run side by side on one XCD and share its L2.
+  // in order.  With a 1-D grid, id L is slot L / 8 of XCD L % 8, and XCD x owns the slots
+  // x * G / 8 .. (x + 1) * G / 8 - 1 of the (part, head block) sequence, head blocks of a part
+  // adjacent.  So the workgroups that read the same query rows (the splits and head blocks of
+  // one sequence: consecutive parts) and the same pages (the head blocks of one part) run on
+  // one XCD, together, and share its L2.
   int part, hb;
-  if (p.xcd_hb > 1) {
+  if (p.xcd_hb > 0) {
     const int L = blockIdx.x;
-    const int slot = L >> 3;
+    const int slot = (L & 7) * (int)(gridDim.x >> 3) + (L >> 3);
     hb = slot % p.xcd_hb;
-    part = (slot / p.xcd_hb) * 8 + (L & 7);
+    part = slot / p.xcd_hb;
   } else {
     part = blockIdx.x;
     hb = blockIdx.y;
@@ -1476,7 +1479,6 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   };
 
   const int kv_st = (int)p.kv_st, kr_st = (int)p.kr_st;
-  const bool paged = p.block_table != nullptr;
 
 #pragma unroll 1
   for (; b < p.batch; ++b, page = 0, split = 0) {
@@ -1488,6 +1490,11 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     const int st_end_seq = (L + kStageTok - 1) / kStageTok;
     const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
     const int nst = st_end > st_begin ? st_end - st_begin : 0;
+    // formed per segment from an opaque copy (hoisted, the flag was spilled to scratch and its
+    // reload waited for the query loads in flight)
+    int paged_i = p.block_table != nullptr;
+    asm volatile("" : "+v"(paged_i));
+    const bool paged = __builtin_amdgcn_readfirstlane(paged_i) != 0;
 
     int pbase = 0, bt_lane = 0;
 
@@ -1502,18 +1509,23 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
       }
     };
     // ---- query fragments of this wave's rows (B operand of S^T = K Q^T), resident for the
-    // segment; rows past the end re-load the last row (their results are never written)
+    // segment; rows past the end re-load the last row (their results are never written).
+    // The addresses come from an opaque copy of the lane id: otherwise their row-dependent
+    // parts are hoisted out of the segment loop and spilled, and each reload (on the in-order
+    // vmcnt) waits for every load issued before it, a memory round trip apiece.
+    int lq = lane;
+    asm volatile("" : "+v"(lq));
     i32x4 qf[HT][kKSteps];
     int lim[HT];
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
-      int row = row0 + 16 * ht + li;
+      int row = row0 + 16 * ht + (lq & 15);
       row = row < p.rows ? row : p.rows - 1;
       const int s = row / p.heads;
       const int h = row - s * p.heads;
       lim[ht] = L - (p.causal ? (p.s_q - 1 - s) : 0);
-      const uint16_t* qn = p.q_nope + (b * p.q_sb + s * p.q_ss + h * p.q_sh) + 16 * g;
-      const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 16 * g;
+      const uint16_t* qn = p.q_nope + (b * p.q_sb + s * p.q_ss + h * p.q_sh) + 16 * (lq >> 4);
+      const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 16 * (lq >> 4);
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
         const int d = 64 * (kk >> 1) + 8 * (kk & 1);  // dims 8*sigma(kk, g)
@@ -1633,7 +1645,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         for (int ht = 0; ht < HT; ++ht) m_ref[ht] = -INFINITY;
       }
       if constexpr (MODE == kPassFirstStageRef) {
-        if (wave == 0) over_sh[lane & 3] = 0;  // uniform branch; ordered by the first barrier
+        if (wave == 0) over_sh[lq & 3] = 0;  // uniform branch; ordered by the first barrier
       }
       load_page_ids(page);
       wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
@@ -2896,7 +2908,7 @@ bool wide_enabled() {
 
 template <int DT, int HT>
 hipError_t launch_wide(const mla::KParams& kp, int head_blocks, hipStream_t st) {
-  if (head_blocks > 1 && kp.num_parts % 8 == 0) {  // head blocks of a part side by side on one XCD
+  if ((kp.num_parts * head_blocks) % 8 == 0) {  // XCD-blocked 1-D grid (see the kernel)
     mla::KParams k = kp;
     k.xcd_hb = head_blocks;
     hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT>), dim3(kp.num_parts * head_blocks), dim3(256), 0, st, k);

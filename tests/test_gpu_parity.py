@@ -340,13 +340,14 @@ def test_reference_contiguous_layout(gpu, kv_ctx, monkeypatch):
 
 
 @pytest.mark.parametrize("kv_ctx", [100, 4096])
-def test_reference_factories_and_run_kernel(gpu, kv_ctx, monkeypatch):
+@pytest.mark.parametrize("h", [64, 128])
+def test_reference_factories_and_run_kernel(gpu, kv_ctx, h, monkeypatch):
     """The explicit-config factories (mla_decode.py:33-39, :263; called by
     scripts/bench_mla_heads.py:130-136 with TileLang knobs) and run_kernel (:715-717)."""
     import mla_decode
     monkeypatch.setattr(mla_decode, "_AUTOTUNE_ENABLED", False)
-    g = torch.Generator().manual_seed(kv_ctx + 1)
-    b, h = 2, 64
+    g = torch.Generator().manual_seed(kv_ctx + h)
+    b = 2
     mk = lambda *s: (torch.randn(*s, generator=g) * 0.1).to(torch.float16)  # noqa: E731
     q, q_pe, kv, k_pe = mk(b, h, 512), mk(b, h, 64), mk(b, kv_ctx, 1, 512), mk(b, kv_ctx, 1, 64)
     ref = R.decode_contiguous(q, q_pe, kv, k_pe)
