@@ -1490,6 +1490,9 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     const int st_end_seq = (L + kStageTok - 1) / kStageTok;
     const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
     const int nst = st_end > st_begin ? st_end - st_begin : 0;
+    // the sequence's workspace slots, loaded here so that the epilogue does not wait on them
+    const int slot0 = p.splits[b];
+    const bool single = (p.splits[b + 1] - slot0) == 1;
     // formed per segment from an opaque copy (hoisted, the flag was spilled to scratch and its
     // reload waited for the query loads in flight)
     int paged_i = p.block_table != nullptr;
@@ -1928,11 +1931,14 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     // publishes 1 / (row sum); then every wave normalises its dims of all R rows.  Branch-free
     // apart from uniform branches; padding rows (past the last row) compute and store the last
     // row's values.
-    const int slot0 = p.splits[b];
-    const bool single = (p.splits[b + 1] - slot0) == 1;
     const int64_t slot = slot0 + split;
+    // Opaque copies of the lane id and the head count: the (row -> token, head) division below
+    // otherwise reuses a constant formed at kernel start, spilled, whose reload in each row
+    // tile waits (in-order vmcnt) for every store issued before it.
     int lane_e = lane;
     asm volatile("" : "+v"(lane_e));
+    int heads_e = p.heads;
+    asm volatile("" : "+v"(heads_e));
     const int li_e = lane_e & 15, g_e = lane_e >> 4;
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
@@ -1942,40 +1948,41 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
       row = row < p.rows ? row : p.rows - 1;
       inv_sh[wave * 16 * HT + 16 * ht + li_e] = l > 0.f ? 1.f / l : 0.f;  // four lane groups, one value
       const float lse2 = lx > 0.f ? m_ref[ht] + __log2f(lx) : -INFINITY;
-      const int s = row / p.heads;
-      const int h = row - s * p.heads;
+      const int s = row / heads_e;
+      const int h = row - s * heads_e;
       if (single) {
-        if (p.lse != nullptr) p.lse[((int64_t)b * p.heads + h) * p.s_q + s] = lse2 * kLn2;
+        if (p.lse != nullptr) p.lse[((int64_t)b * heads_e + h) * p.s_q + s] = lse2 * kLn2;
       } else {
         p.ws_lse[slot * p.rows + row] = lse2;
       }
     }
     wait_lgkm0();
     lds_barrier();
+    // The wave's 128 dims of all R rows go out through its 32 KiB quarter of the latent ring
+    // (free after the pass): packed to 16 bits and written there in rows of 256 bytes, then
+    // read back so that each global store writes four whole row slices, 16 bytes per lane and
+    // eight full cache lines per instruction.  Stored straight from the fragment layout, each
+    // instruction wrote 32-byte pieces of 16 lines, and the store path took ~60 cycles per
+    // instruction: ~2000 per row tile.  In the staging rows, 32-byte chunk c of row r sits at
+    // chunk c ^ (r % 8), so the 16 rows of one fragment write fall on 8 chunk positions.
+    uint8_t LDS_AS* const stg = lat + wave * (32 * 1024);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const float inv = inv_sh[16 * rt + li];
-      int row = rowb + 16 * rt + li_e;
-      row = row < p.rows ? row : p.rows - 1;
-      if (single) {  // uniform
-        const int s = row / p.heads;
-        const int h = row - s * p.heads;
-        uint16_t* dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 128 * wave + 4 * g_e;
-#pragma unroll
-        for (int t = 0; t < WDT; ++t) {  // dims 128w + 64*(t%2) + 16*(t/2) + 4g ..
-          const f32x4 v = o[t][rt] * inv;
-          *(i32x2*)(dst + 64 * (t & 1) + 16 * (t >> 1)) =
-              i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
-        }
-      } else if (p.part16) {  // uniform
-        uint16_t* dst = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * g_e;
+      const float inv = inv_sh[16 * rt + li_e];
+      const int r = 16 * rt + li_e;  // row of the workgroup
+      // bits 5-7 of the row's LDS address are zero, so the chunk permutation is one XOR
+      const uint32_t srow = (uint32_t)(uintptr_t)(stg + r * 256 + 8 * g_e) ^ (uint32_t)((r & 7) << 5);
+      // fragment t holds dims 64*(t%2) + 16*(t/2) + 4g .. +3 of the slice: chunk 4*(t%2) + t/2
+      auto put = [&](int t, const i32x2 v) __attribute__((always_inline)) {
+        *(i32x2 LDS_AS*)(uintptr_t)(srow ^ (uint32_t)((4 * (t & 1) + (t >> 1)) << 5)) = v;
+      };
+      if (single || p.part16) {  // uniform
 #pragma unroll
         for (int t = 0; t < WDT; ++t) {
           const f32x4 v = o[t][rt] * inv;
-          *(i32x2*)(dst + 64 * (t & 1) + 16 * (t >> 1)) =
-              i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])};
+          put(t, i32x2{(int)pack2<DT>(v[0], v[1]), (int)pack2<DT>(v[2], v[3])});
         }
-      } else {  // scaled fp16: the wave's chunk of row li spans the four lane groups
+      } else {  // scaled fp16: the wave's chunk of row r spans the four lane groups
         float am = 0.f;
 #pragma unroll
         for (int t = 0; t < WDT; ++t) am = fmaxf(am, amax4(o[t][rt]));
@@ -1983,16 +1990,62 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         am = fmaxf(am, __shfl_xor(am, 16));
         am = fmaxf(am, __shfl_xor(am, 32));
         const int e = part_exp(am);
-        uint16_t* dst = p.ws_o + (slot * p.rows + row) * kDV + 128 * wave + 4 * g_e;
+        const float f = inv * exp2i(e);  // o * (inv * 2^e) rounds exactly as (o * inv) * 2^e
 #pragma unroll
         for (int t = 0; t < WDT; ++t) {
-          const f32x4 v = (o[t][rt] * inv) * exp2i(e);
-          *(i32x2*)(dst + 64 * (t & 1) + 16 * (t >> 1)) =
-              i32x2{(int)pack2<MLA_DTYPE_F16>(v[0], v[1]), (int)pack2<MLA_DTYPE_F16>(v[2], v[3])};
+          const f32x4 v = o[t][rt] * f;
+          put(t, i32x2{(int)pack2<MLA_DTYPE_F16>(v[0], v[1]), (int)pack2<MLA_DTYPE_F16>(v[2], v[3])});
         }
+        int row = rowb + r;
+        row = row < p.rows ? row : p.rows - 1;
         p.ws_scale[(slot * p.rows + row) * 4 + wave] = exp2i(-e);  // four lane groups, one value
       }
     }
+    // rows 4j .. 4j+3: lane l moves bytes 16*(l%16) .. +15 of row 4j + l/16 (this wave's own
+    // staging rows: no barrier, LDS runs one wave's accesses in order)
+    {
+      const int q = lane_e & 15;
+      const int r0 = lane_e >> 4;
+      auto staged = [&](int j) __attribute__((always_inline)) {
+        const int r = 4 * j + r0;
+        return *(const i32x4 LDS_AS*)(stg + r * 256 + ((((q >> 1) ^ (r & 7)) << 5) | ((q & 1) << 4)));
+      };
+      // uniform: the workgroup's rows are one run of rows in the destination (no padding rows,
+      // one query token), so row r is at a fixed stride from row 0
+      const bool linear = rowb + R <= p.rows && (!single || (rowb % heads_e) + R <= heads_e);
+      if (linear) {
+        int64_t stride;
+        uint16_t* dst;
+        if (single) {
+          const int s = rowb / heads_e;
+          const int h = rowb - s * heads_e + r0;
+          dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh) + 128 * wave + 8 * q;
+          stride = 4 * p.o_sh;
+        } else {
+          dst = p.ws_o + (slot * p.rows + rowb + r0) * kDV + 128 * wave + 8 * q;
+          stride = 4 * kDV;
+        }
+#pragma unroll 4
+        for (int j = 0; j < R / 4; ++j) *(i32x4*)(dst + j * stride) = staged(j);
+      } else {
+#pragma unroll 2
+        for (int j = 0; j < R / 4; ++j) {
+          int row = rowb + 4 * j + r0;
+          row = row < p.rows ? row : p.rows - 1;  // padding rows repeat the last row's values
+          uint16_t* dst;
+          if (single) {  // uniform
+            const int s = row / heads_e;
+            const int h = row - s * heads_e;
+            dst = p.out + (b * p.o_sb + s * p.o_ss + h * p.o_sh);
+          } else {
+            dst = p.ws_o + (slot * p.rows + row) * kDV;
+          }
+          *(i32x4*)(dst + 128 * wave + 8 * q) = staged(j);
+        }
+      }
+    }
+    wait_lgkm0();
+    lds_barrier();  // the staging reads are done before the next segment's loads refill the ring
     // inv_sh is rewritten only after the next segment's barriers
   }
 }

@@ -86,6 +86,22 @@ def test_tails_all_head_counts(gpu, H, dtype):
         assert_parity(out, lse, ref_o, ref_l, f"H={H} ns={ns}")
 
 
+@pytest.mark.parametrize("H, s_q", [(40, 1), (48, 2), (96, 1), (40, 2), (80, 2)])
+def test_head_counts_off_the_row_tile(gpu, H, s_q):
+    """Row counts s_q*H that are not a multiple of the wide kernel's 64- or 128-row workgroup
+    (padding rows), and head blocks whose rows span both query tokens: the general
+    (row-by-row) store path of the epilogue, for direct outputs and for split partials."""
+    lengths = [1, 33, 64, 65, 700, 2100]
+    cfg = small_cfg(f"odd_h{H}_sq{s_q}", len(lengths), s_q, H, lengths)
+    inp = make_inputs(cfg, seed=H + s_q)
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                  inp.sm_scale, inp.causal)
+    for ns in (None, 1, 3):
+        say(f"odd heads H={H} s_q={s_q} num_splits={ns}")
+        out, lse = run_paged(inp, gpu, ns)
+        assert_parity(out, lse, ref_o, ref_l, f"H={H} s_q={s_q} ns={ns}")
+
+
 @pytest.mark.parametrize("H", [16, 64, 128])
 def test_causal_two_queries(gpu, H):
     lengths = [1, 2, 33, 64, 65, 300]
