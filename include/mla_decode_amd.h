@@ -158,11 +158,13 @@ const char* mla_last_error(void);
 int mla_num_parts(int32_t batch, int32_t s_q, int32_t heads_q, int32_t heads_k, int32_t cu_count);
 
 /*
- * Kernel tile chosen for `rows` = s_q * heads_q query rows: waves per workgroup, 16-row tiles
- * per wave, LDS stages of 32 tokens in flight per ring, rows per workgroup.  When
- * rows_per_workgroup is 16 * row_tiles (less than waves * 16 * row_tiles), the waves share one
- * row tile and take turns over the KV stages, each with its own one-stage ring, and merge their
- * results at the end of every segment.  Returns 0, or
+ * Kernel tile chosen for `rows` = s_q * heads_q query rows (dense bf16/fp16 cache): waves per
+ * workgroup, 16-row tiles per wave (of the QK product), LDS stages of 32 tokens resident per
+ * ring, rows per workgroup.  Above 32 rows this is the wide kernel (PV split by output dims
+ * across the waves, a 4-stage latent ring); when rows_per_workgroup is 16 * row_tiles (less
+ * than waves * 16 * row_tiles), the waves share one row tile and take turns over the KV
+ * stages, each with its own one-stage ring, and merge their results at the end of every
+ * segment.  Returns 0, or
  * MLA_ERR_INVALID for rows < 1 or a NULL output.  Replaces the block_H / threads / stages
  * fields of the tuned-config record (mla_best_configs.json:1-73).
  */

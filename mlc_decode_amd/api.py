@@ -22,6 +22,7 @@ int32, cache_seqlens ``[B]`` int32, out ``[B, s_q, H, 512]`` in q's dtype and ls
 from __future__ import annotations
 
 import ctypes
+import os
 import math
 import threading
 from typing import NamedTuple, Optional, Sequence, Tuple, Union
@@ -88,7 +89,9 @@ def kernel_variant(rows: int) -> dict:
     w, t, st, r = (ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32())
     check("mla_variant", _lib.load().mla_variant(rows, ctypes.byref(w), ctypes.byref(t),
                                                   ctypes.byref(st), ctypes.byref(r)))
-    return {"waves": w.value, "row_tiles_per_wave": t.value, "lds_stages": st.value,
+    kernel = ("mla_wide_kernel" if rows > 32 and os.environ.get("MLA_WIDE", "1") != "0"
+              else "mla_splitkv_kernel")
+    return {"kernel": kernel, "waves": w.value, "row_tiles_per_wave": t.value, "lds_stages": st.value,
             "rows_per_workgroup": r.value, "stage_tokens": 32}
 
 

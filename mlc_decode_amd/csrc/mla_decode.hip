@@ -3142,7 +3142,7 @@ int mla_variant(int32_t rows, int32_t* waves, int32_t* row_tiles, int32_t* stage
   const Variant v = pick_variant(rows);
   *waves = v.nw;
   *row_tiles = v.ht;
-  *stages = v.nstage;
+  *stages = (!v.ws && v.nw == 4 && wide_enabled()) ? mla::kWideLat : v.nstage;  // the wide kernel's ring
   *rows_per_workgroup = v.rows();
   return MLA_OK;
 }

@@ -142,8 +142,9 @@ def test_variant_query(lib):
     ptrs = [ctypes.byref(v) for v in vals]
     assert lib.mla_variant(16, *ptrs) == 0 and [v.value for v in vals] == [4, 1, 1, 16]
     assert lib.mla_variant(32, *ptrs) == 0 and [v.value for v in vals] == [1, 2, 1, 32]
+    # above 32 rows the wide kernel runs (MLA_WIDE unset): its latent ring holds 4 stages
     assert lib.mla_variant(64, *ptrs) == 0 and [v.value for v in vals] == [4, 1, 4, 64]
-    assert lib.mla_variant(128, *ptrs) == 0 and [v.value for v in vals] == [4, 2, 3, 128]
+    assert lib.mla_variant(128, *ptrs) == 0 and [v.value for v in vals] == [4, 2, 4, 128]
     assert lib.mla_variant(0, *ptrs) == 1
 
 
