@@ -102,6 +102,32 @@ def test_head_counts_off_the_row_tile(gpu, H, s_q):
         assert_parity(out, lse, ref_o, ref_l, f"H={H} s_q={s_q} ns={ns}")
 
 
+_RANDOM_HEADS = [1, 3, 8, 16, 24, 31, 40, 48, 64, 72, 96, 128, 136, 160]
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_shapes(gpu, case):
+    """Seeded random decodes across every kernel variant and grid form: head counts on and
+    off the 16/32/64/128-row tiles (several head blocks above 128 rows), s_q 1 and 2, empty,
+    one-token and page-straddling lengths, bf16 and fp16, the scheduler and forced splits."""
+    rnd = random.Random(1000 + case)
+    H = rnd.choice(_RANDOM_HEADS)
+    s_q = rnd.choice([1, 1, 2])
+    B = rnd.randint(1, 24)
+    lengths = [rnd.choice([0, 1, 31, 64, 65, rnd.randint(1, 600), rnd.randint(600, 2600)]) for _ in range(B)]
+    if max(lengths) == 0:
+        lengths[0] = 17
+    dtype = rnd.choice([torch.bfloat16, torch.float16])
+    ns = rnd.choice([None, None, 1, rnd.randint(2, 6)])
+    cfg = small_cfg(f"rand{case}", B, s_q, H, lengths, dtype)
+    inp = make_inputs(cfg, seed=case)
+    say(f"random case {case}: B={B} s_q={s_q} H={H} dtype={dtype} num_splits={ns} lengths={lengths}")
+    out, lse = run_paged(inp, gpu, ns)
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                  inp.sm_scale, inp.causal)
+    assert_parity(out, lse, ref_o, ref_l, f"random case {case}")
+
+
 @pytest.mark.parametrize("H", [16, 64, 128])
 def test_causal_two_queries(gpu, H):
     lengths = [1, 2, 33, 64, 65, 300]
