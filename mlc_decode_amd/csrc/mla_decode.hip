@@ -1382,25 +1382,6 @@ constexpr int kLatStageBytes = 32 * 1024;    // 32 token rows x 512 dims
 constexpr int kRopeStageBytes = 4 * 1024;    // 32 token rows x 64 dims
 constexpr int kWidePanel = 16 * 1024;        // tokens 16..31 of a latent stage
 
-// Wave w loads row group w of a stage: 8 latent blocks and 1 rope block, each one
-// global_load_lds_dwordx4 whose eight lanes per row cover one 128-byte line.  Rows past the
-// sequence end re-read its last row (in bounds, masked later).
-__device__ __forceinline__ void issue_stage_wide(uint8_t LDS_AS* lat, uint8_t LDS_AS* rope,
-                                                 const uint16_t* nope_base, const uint16_t* rope_base,
-                                                 int kv_st, int kr_st, int last_row, int wave, int lane) {
-  const int q = wave;  // uniform
-  int row = 8 * q + (lane >> 3);
-  row = row < last_row ? row : last_row;
-  const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((q & 1) << 3) | (lane >> 3))) << 4);
-  const uint32_t on = (uint32_t)(row * kv_st) * 2 + cl;
-  const uint32_t orp = (uint32_t)(row * kr_st) * 2 + cl;
-  uint8_t LDS_AS* dst = lat + q * 8 * 1024;
-#pragma unroll
-  for (int sg = 0; sg < 8; ++sg)
-    dma16((const char*)nope_base + 128 * sg, on, (uint32_t)(uintptr_t)(dst + sg * 1024));
-  dma16(rope_base, orp, (uint32_t)(uintptr_t)(rope + q * 1024));
-}
-
 template <int DT, int HT>
 __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   constexpr int NW = 4;
