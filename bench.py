@@ -85,19 +85,24 @@ def settle_clocks(fn, stream, seconds=0.25):
 FLUSH_BYTES = 1 << 30  # larger than the L2s and the 256 MB MALL together
 
 
-def time_cold(fn, reps, stream):
-    """Median ms of single calls, each after a 1 GiB fill that evicts the caches.  The fill
-    runs long enough for the host to queue the call behind it, so the GPU does not wait on
-    the host between the two events."""
+def time_cold(fn, reps, stream, dirty=False):
+    """Median ms of single calls, each after a 1 GiB sweep that evicts the caches.  The default
+    sweep reads (a sum), so the caches hold clean lines; with ``dirty`` it writes (a fill), so
+    the call's first misses also pay for writing back the dirty lines the fill left in L2 and
+    MALL.  The sweep runs long enough for the host to queue the call behind it, so the GPU does
+    not wait on the host between the two events."""
     import statistics
 
     import torch
-    junk = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda:0")
+    junk = torch.ones(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda:0")
     fn()
     torch.cuda.synchronize()
     times = []
     for _ in range(reps):
-        junk.fill_(1)
+        if dirty:
+            junk.fill_(1)
+        else:
+            junk.sum()
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record(stream)
@@ -193,6 +198,7 @@ def measure(cfg_name, steps, warmup, kv_fp8=False, cold=True):
 
     ms_e2e = time_gpu(end_to_end, steps, warmup, stream)
     ms_cold = None if not cold else time_cold(call, max(10, min(steps, 40)), stream)
+    ms_cold_dirty = None if not cold else time_cold(call, max(10, min(steps, 40)), stream, dirty=True)
     del keep
 
     nbytes = algorithmic_bytes(cpu_inp.cache_seqlens, B, s_q, H, 2)
@@ -209,7 +215,8 @@ def measure(cfg_name, steps, warmup, kv_fp8=False, cold=True):
     call_frac = (nbytes / (ms_call * 1e-3) / 1e9 / HBM_PEAK_GBS if bound == "hbm"
                  else flops / (ms_call * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS)
     return dict(cfg=cfg, cpu_inp=cpu_inp, ms_call=ms_call, ms_main=ms_main, ms_combine=ms_combine,
-                ms_meta=ms_meta, ms_e2e=ms_e2e, ms_cold=ms_cold, nbytes=nbytes, flops=flops,
+                ms_meta=ms_meta, ms_e2e=ms_e2e, ms_cold=ms_cold, ms_cold_dirty=ms_cold_dirty,
+                nbytes=nbytes, flops=flops,
                 bound=bound, gbs=gbs, tflops=tflops, call_frac=call_frac,
                 parts=int(sched.shape[0]), n_splits=n_splits)
 
@@ -458,6 +465,7 @@ def main():
                      "us_metadata": round(mm["ms_meta"] * 1e3, 2),
                      "us_end_to_end": round(mm["ms_e2e"] * 1e3, 2),
                      "us_call_cold": None if mm["ms_cold"] is None else round(mm["ms_cold"] * 1e3, 2),
+                     "us_call_cold_dirty": None if mm["ms_cold_dirty"] is None else round(mm["ms_cold_dirty"] * 1e3, 2),
                      "call_frac": round(mm["call_frac"], 4),
                      "tbps": round(mm["gbs"] / 1e3, 3), "tflops": round(mm["tflops"], 1),
                      "bound": mm["bound"], "roofline_frac": round(frac, 4),
@@ -505,6 +513,7 @@ def main():
         "metadata_us": round(m["ms_meta"] * 1e3, 3),
         "us_end_to_end_with_metadata": round(m["ms_e2e"] * 1e3, 3),
         "us_call_cold": None if m["ms_cold"] is None else round(m["ms_cold"] * 1e3, 3),
+        "us_call_cold_dirty": None if m["ms_cold_dirty"] is None else round(m["ms_cold_dirty"] * 1e3, 3),
         "call_roofline_frac": round(m["call_frac"], 4),
         "stream_probe_gbs": probe,
         "frac_of_measured_peak": (round(m["gbs"] / probe["best"], 4) if m["bound"] == "hbm" and probe else None),
