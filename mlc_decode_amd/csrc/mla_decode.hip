@@ -2222,6 +2222,60 @@ __device__ __forceinline__ float merge_splits_wave(const PT* __restrict__ ws_o, 
   return lse2;
 }
 
+// merge_splits_wave for a row of at most kFewSplits 16-bit partials, in one memory round trip:
+// the lse values, partial rows and chunk scales of all its splits are requested together (the
+// partials do not depend on the weights), then merged with merge_splits_wave's arithmetic
+// operation for operation, so the result is bit-identical: the same max, the same sum in the
+// order of its xor butterfly (splits k >= n contribute zeros, which leave every partial sum
+// unchanged), the same weights and the same fma chain in split order.
+constexpr int kFewSplits = 8;
+template <int DT, bool SCALED>
+__device__ __forceinline__ float merge_few_splits(const uint16_t* __restrict__ ws_o, const float* __restrict__ ws_scale,
+                                                  const float* __restrict__ ws_lse, int base, int n, int rows,
+                                                  int row, int lane, float (&acc)[8]) {
+  constexpr int LDT = SCALED ? MLA_DTYPE_F16 : DT;
+  const uint16_t* src0 = ws_o + ((int64_t)base * rows + row) * kDV + lane * 8;
+  const int64_t split_stride = (int64_t)rows * kDV;
+  const float* sc0 = SCALED ? ws_scale + ((int64_t)base * rows + row) * 4 + (lane >> 4) : nullptr;
+  const int64_t sc_stride = (int64_t)rows * 4;
+  float l[kFewSplits], us[kFewSplits];
+  i32x4 raw[kFewSplits];
+#pragma unroll
+  for (int k = 0; k < kFewSplits; ++k) {
+    l[k] = -INFINITY;
+    us[k] = 1.f;
+    raw[k] = i32x4{0, 0, 0, 0};
+    if (k < n) {  // uniform
+      l[k] = ws_lse[(int64_t)(base + k) * rows + row];
+      raw[k] = *(const i32x4*)(src0 + k * split_stride);
+      if constexpr (SCALED) us[k] = sc0[k * sc_stride];
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kFewSplits; ++k) mx = fmaxf(mx, l[k]);
+  float e[kFewSplits];
+#pragma unroll
+  for (int k = 0; k < kFewSplits; ++k) e[k] = (mx != -INFINITY && k < n) ? fast_exp2(l[k] - mx) : 0.f;
+  // the butterfly's association: offsets 32, 16 and 8 add zeros, then 4, 2, 1
+  const float sum = ((e[0] + e[4]) + (e[2] + e[6])) + ((e[1] + e[5]) + (e[3] + e[7]));
+  const float lse2 = sum > 0.f ? mx + __log2f(sum) : -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+#pragma unroll
+  for (int k = 0; k < kFewSplits; ++k) {
+    if (k < n) {  // uniform
+      float x[8];
+      cvt8<LDT>(raw[k], x);
+      const float w = lse2 != -INFINITY ? fast_exp2(l[k] - lse2) : 0.f;
+      const float wk = w * us[k];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += wk * x[j];
+    }
+  }
+  return lse2;
+}
+
 // One wave per (sequence, row).
 template <int DT, typename PT, bool SCALED>
 __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__ ws_o,
@@ -2243,8 +2297,15 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__
   const int n = splits[b + 1] - base;
   if (n < 1 || (n == 1 && !copy_single)) return;
   float acc[8];
-  const float lse2 = merge_splits_wave<DT, PT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane,
-                                                       w_sh[wave], acc);
+  float lse2;
+  if constexpr (std::is_same<PT, uint16_t>::value) {
+    if (n <= kFewSplits)  // uniform
+      lse2 = merge_few_splits<DT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane, acc);
+    else
+      lse2 = merge_splits_wave<DT, PT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane, w_sh[wave], acc);
+  } else {
+    lse2 = merge_splits_wave<DT, PT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane, w_sh[wave], acc);
+  }
   const int s = row / heads;
   const int h = row - s * heads;
   uint16_t* dst = out + b * o_sb + s * o_ss + h * o_sh + lane * 8;
