@@ -559,6 +559,10 @@ void mla_splitkv_kernel(KParams p) {
   // every fragment on its way to the MFMA instead (kInl8).
   constexpr bool kDeq = KV8 && NL == 4;
   constexpr bool kInl8 = KV8 && !kDeq;
+  // wave split, dense 16-bit cache: a wave refills its slot with its next own stage while it
+  // still computes the current one (rope blocks after QK, each 64-dim latent segment once PV
+  // has read it), instead of in one burst after PV
+  constexpr bool kProg = WS && !KV8 && !SPARSE;
   __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSmem + (kDeq ? kStageBytes : 0)];
   // wave-split merge words: (row max, row sum of rounded P, row sum of fp32 P) per wave and row
   __shared__ float merge_sh[WS ? NW : 1][3][16];
@@ -739,6 +743,50 @@ void mla_splitkv_kernel(KParams p) {
                       (left < kStageTok ? left : kStageTok) - 1, NL == 1 ? 0 : wave, lane);
     };
 
+    // kProg: the loads of issue_stage<1> for stage k, in parts: prog_prepare forms the bases
+    // and per-lane offsets once, prog_rope issues the four rope blocks, prog_seg(s) the four
+    // blocks of latent segment s (block q*9 + s: rows 8q .. 8q+7, chunks 8s .. 8s+7)
+    struct ProgLoads {
+      const uint16_t* nb;
+      const uint16_t* rb;
+      uint32_t on[4], orp[4];
+    };
+    auto prog_prepare = [&](int k) __attribute__((always_inline)) {
+      ProgLoads r;
+      const int st = st_begin + k;
+      if (paged) {
+        const int pidx = st >> 1;
+        if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
+        const int pg = __builtin_amdgcn_readlane(bt_lane, pidx - pbase);
+        const int tok = (st & 1) * kStageTok;
+        r.nb = p.kv_nope + ((int64_t)pg * p.kv_sp + tok * kv_st);
+        r.rb = p.kv_rope + ((int64_t)pg * p.kr_sp + tok * kr_st);
+      } else {
+        r.nb = p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st * kStageTok * kv_st);
+        r.rb = p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st);
+      }
+      const int left = L - st * kStageTok;
+      const int last_row = (left < kStageTok ? left : kStageTok) - 1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int row = 8 * q + (lane >> 3);
+        row = row < last_row ? row : last_row;  // rows past the sequence end re-read its last row
+        const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((q & 1) << 3) | (lane >> 3))) << 4);
+        r.on[q] = (uint32_t)(row * kv_st) * 2 + cl;
+        r.orp[q] = (uint32_t)(row * kr_st) * 2 + cl;
+      }
+      return r;
+    };
+    auto prog_rope = [&](const ProgLoads& r) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dma16(r.rb, r.orp[q], (uint32_t)(uintptr_t)(ring + (q * 9 + 8) * 1024));
+    };
+    auto prog_seg = [&](const ProgLoads& r, int sgm) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        dma16((const char*)r.nb + 128 * sgm, r.on[q], (uint32_t)(uintptr_t)(ring + (q * 9 + sgm) * 1024));
+    };
+
     // One pass over the segment's stages.  Returns true (uniformly across the workgroup)
     // when a first-stage-reference pass saw a score above its reference by more than tau.
     auto run_pass = [&](auto mode_tag) __attribute__((always_inline)) -> bool {
@@ -773,7 +821,7 @@ void mla_splitkv_kernel(KParams p) {
       // sharing it has consumed the current one; latency is hidden by the other waves of the
       // CU instead.
       auto refill_single = [&](int k) __attribute__((always_inline)) {
-        if constexpr (NSTAGE == 1) {
+        if constexpr (NSTAGE == 1 && !(kProg && MODE != kPassRowMax)) {
           if constexpr (NW > 1 && !WS) lds_barrier();
           if (k + kStep < nst) issue(k + kStep);
         }
@@ -793,20 +841,33 @@ void mla_splitkv_kernel(KParams p) {
         return lds_tr_pair(xb + (t & 7) * 1024);
       };
       // the first DV V^T fragments of stage kp (issued ahead of the softmax to hide latency)
+      // kProg: tiles in segment-major order (dt = t), so segment s is read by tiles 4s .. 4s+3
+      // and refilled (`seg`) once the last of them has issued: every read of it has landed,
+      // since each fragment is awaited before the MFMA that takes it
+      auto v_frag_s = [&](const uint8_t LDS_AS* vb, int t) __attribute__((always_inline)) {
+        const uint8_t LDS_AS* xb =
+            (t & 3) ? (const uint8_t LDS_AS*)(uintptr_t)((uint32_t)(uintptr_t)vb ^ (uint32_t)(32 * (t & 3))) : vb;
+        return lds_tr_pair(xb + (t >> 2) * 1024);
+      };
       auto v_prefetch = [&](int kp, i32x4 (&vf)[DV]) __attribute__((always_inline)) {
         const uint8_t LDS_AS* vb = v_base(kp);
 #pragma unroll
-        for (int n = 0; n < DV; ++n) vf[n] = v_frag(vb, n);
+        for (int n = 0; n < DV; ++n) vf[n] = kProg ? v_frag_s(vb, n) : v_frag(vb, n);
       };
-      auto pv_stage = [&](int kp, i32x4 (&pb)[HT], i32x4 (&vf)[DV]) __attribute__((always_inline)) {
+      auto pv_stage = [&](int kp, i32x4 (&pb)[HT], i32x4 (&vf)[DV], auto prog_tag, const auto& seg)
+                          __attribute__((always_inline)) {
+        constexpr bool kP = decltype(prog_tag)::value;
         const uint8_t LDS_AS* vb = v_base(kp);
 #pragma unroll
         for (int t = 0; t < kDimTiles; ++t) {
-          const int dt = 4 * (t & 7) + (t >> 3);
+          const int dt = kP ? t : 4 * (t & 7) + (t >> 3);
           const i32x4 a = vf[t % DV];
-          if (t + DV < kDimTiles) vf[t % DV] = v_frag(vb, t + DV);
+          if (t + DV < kDimTiles) vf[t % DV] = kP ? v_frag_s(vb, t + DV) : v_frag(vb, t + DV);
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) o[dt][ht] = mfma32<DT>(a, pb[ht], o[dt][ht]);
+          if constexpr (kP) {
+            if ((t & 3) == 3) seg(t >> 2);
+          }
           __builtin_amdgcn_sched_barrier(0);
         }
         // The last MFMAs are still reading their A/B operands (P^T and the last V^T fragment)
@@ -1059,6 +1120,15 @@ void mla_splitkv_kernel(KParams p) {
           if constexpr (kInl8) v8_prefetch(k, vr);
           else v_prefetch(k, vf);
         }
+        // kProg: the next own stage's loads, rope now (QK has read it), latent during PV
+        const bool prog_next = kProg && MODE != kPassRowMax && k + kStep < nst;  // uniform
+        ProgLoads prog{};
+        if constexpr (kProg && MODE != kPassRowMax) {
+          if (prog_next) {
+            prog = prog_prepare(k + kStep);
+            prog_rope(prog);
+          }
+        }
 
         // ---- sparse: mask the stage's tokens whose index is past the list or outside the pool
         if constexpr (SPARSE) {
@@ -1157,8 +1227,15 @@ void mla_splitkv_kernel(KParams p) {
           }
         }
 
-        if constexpr (kInl8) pv_stage8(k, pvf, vr);
-        else pv_stage(k, pb, vf);
+        if constexpr (kInl8) {
+          pv_stage8(k, pvf, vr);
+        } else if constexpr (kProg) {
+          pv_stage(k, pb, vf, std::true_type{}, [&](int sgm) __attribute__((always_inline)) {
+            if (prog_next) prog_seg(prog, sgm);
+          });
+        } else {
+          pv_stage(k, pb, vf, std::false_type{}, [](int) {});
+        }
         refill_single(k);
         if constexpr (MODE == kPassFirstStageRef && !WS) wait_lgkm0();  // flag store lands before the barrier
       }
