@@ -965,7 +965,16 @@ void mla_splitkv_kernel(KParams p) {
 #pragma unroll 1
       for (int j = 0, k = k0; k < nst; ++j, k += kStep) {  // j: the wave's own stage count
         const int remaining_after = nst - 1 - k;
-        wait_stage<kLPS / NL, NSTAGE>(remaining_after < LEAD - 1 ? remaining_after : LEAD - 1);
+        // kProg after the first own stage: the stage came in the order rope, segment 0, ..,
+        // segment 7 (four loads each), so QK starts once the rope and segment 0 have landed
+        // and waits for segment s only before its first fragment read (prog_wait)
+        constexpr bool kProgWait = kProg && MODE != kPassRowMax;
+        const bool prog_wait = kProgWait && j > 0;  // uniform
+        if (prog_wait) {
+          wait_vmcnt<28>();
+        } else {
+          wait_stage<kLPS / NL, NSTAGE>(remaining_after < LEAD - 1 ? remaining_after : LEAD - 1);
+        }
         if constexpr (!WS) lds_barrier();
         // the previous stage's flags, read now and tested after this stage's QK product
         int prev_over = 0;
@@ -1085,12 +1094,37 @@ void mla_splitkv_kernel(KParams p) {
             c_cur = c_next;
           }
         } else {
+          // fragment m reads latent segment m / 4 (the rope for m >= 32); the loads of segment
+          // s are awaited before fragment 4s is read (outstanding: the four loads of each later
+          // segment).  In a wave's first own stage nothing is in flight during QK (the stage was
+          // awaited whole and the next one is issued after QK), so the waits cost nothing there.
+          auto seg_wait = [&](int m) __attribute__((always_inline)) {
+            if constexpr (kProgWait) {
+              if ((m & 3) == 0 && m >= 4 && m < 32) {
+                switch (m >> 2) {
+                  case 1: wait_vmcnt<24>(); break;
+                  case 2: wait_vmcnt<20>(); break;
+                  case 3: wait_vmcnt<16>(); break;
+                  case 4: wait_vmcnt<12>(); break;
+                  case 5: wait_vmcnt<8>(); break;
+                  case 6: wait_vmcnt<4>(); break;
+                  default: wait_vmcnt<0>(); break;
+                }
+              }
+            }
+          };
 #pragma unroll
-          for (int n = 0; n < DK; ++n) kf[n] = MLA_KFRAG(n);
+          for (int n = 0; n < DK; ++n) {
+            seg_wait(n);
+            kf[n] = MLA_KFRAG(n);
+          }
 #pragma unroll
           for (int n = 0; n < 2 * kKSteps; ++n) {
             const i32x4 a = kf[n % DK];
-            if (n + DK < 2 * kKSteps) kf[n % DK] = MLA_KFRAG(n + DK);
+            if (n + DK < 2 * kKSteps) {
+              seg_wait(n + DK);
+              kf[n % DK] = MLA_KFRAG(n + DK);
+            }
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) {
               if (n < 2)
