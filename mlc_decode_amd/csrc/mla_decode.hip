@@ -562,7 +562,7 @@ void mla_splitkv_kernel(KParams p) {
   // wave split, dense 16-bit cache: a wave refills its slot with its next own stage while it
   // still computes the current one (rope blocks after QK, each 64-dim latent segment once PV
   // has read it), instead of in one burst after PV
-  constexpr bool kProg = WS && !KV8 && !SPARSE;
+  constexpr bool kProg = WS && !SPARSE;
   __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSmem + (kDeq ? kStageBytes : 0)];
   // wave-split merge words: (row max, row sum of rounded P, row sum of fp32 P) per wave and row
   __shared__ float merge_sh[WS ? NW : 1][3][16];
@@ -746,45 +746,67 @@ void mla_splitkv_kernel(KParams p) {
     // kProg: the loads of issue_stage<1> for stage k, in parts: prog_prepare forms the bases
     // and per-lane offsets once, prog_rope issues the four rope blocks, prog_seg(s) the four
     // blocks of latent segment s (block q*9 + s: rows 8q .. 8q+7, chunks 8s .. 8s+7)
+    // fp8 cache (KV8, paged only): the loads of issue_stage8<1>, the latent in four 128-dim
+    // blocks (prog_seg(s): block s of the four row groups and the stage's 32 scales of block s)
     struct ProgLoads {
-      const uint16_t* nb;
+      const char* nb;
       const uint16_t* rb;
+      const float* scb;
       uint32_t on[4], orp[4];
     };
     auto prog_prepare = [&](int k) __attribute__((always_inline)) {
       ProgLoads r;
+      r.scb = nullptr;
       const int st = st_begin + k;
       if (paged) {
         const int pidx = st >> 1;
         if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
         const int pg = __builtin_amdgcn_readlane(bt_lane, pidx - pbase);
         const int tok = (st & 1) * kStageTok;
-        r.nb = p.kv_nope + ((int64_t)pg * p.kv_sp + tok * kv_st);
+        if constexpr (KV8) {
+          r.nb = (const char*)p.kv_nope + ((int64_t)pg * p.kv_sp + tok * kv_st);
+          r.scb = p.kv_scale + ((int64_t)pg * p.ks_sp + tok);
+        } else {
+          r.nb = (const char*)(p.kv_nope + ((int64_t)pg * p.kv_sp + tok * kv_st));
+        }
         r.rb = p.kv_rope + ((int64_t)pg * p.kr_sp + tok * kr_st);
       } else {
-        r.nb = p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st * kStageTok * kv_st);
+        r.nb = (const char*)(p.kv_nope + ((int64_t)b * p.kv_sb + (int64_t)st * kStageTok * kv_st));
         r.rb = p.kv_rope + ((int64_t)b * p.kr_sb + (int64_t)st * kStageTok * kr_st);
       }
       const int left = L - st * kStageTok;
       const int last_row = (left < kStageTok ? left : kStageTok) - 1;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        int row = 8 * q + (lane >> 3);
-        row = row < last_row ? row : last_row;  // rows past the sequence end re-read its last row
-        const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((q & 1) << 3) | (lane >> 3))) << 4);
-        r.on[q] = (uint32_t)(row * kv_st) * 2 + cl;
-        r.orp[q] = (uint32_t)(row * kr_st) * 2 + cl;
+        const int rr = 8 * q + (lane >> 3);  // LDS row
+        const int row = rr < last_row ? rr : last_row;  // rows past the sequence end re-read its last row
+        if constexpr (KV8) {
+          r.on[q] = (uint32_t)(row * kv_st) + (uint32_t)(((lane & 7) ^ swz8(rr)) << 4);
+          r.orp[q] = (uint32_t)(row * kr_st) * 2 + (uint32_t)(((lane & 7) ^ swzr(rr)) << 4);
+        } else {
+          const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((q & 1) << 3) | (lane >> 3))) << 4);
+          r.on[q] = (uint32_t)(row * kv_st) * 2 + cl;
+          r.orp[q] = (uint32_t)(row * kr_st) * 2 + cl;
+        }
       }
       return r;
     };
     auto prog_rope = [&](const ProgLoads& r) __attribute__((always_inline)) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) dma16(r.rb, r.orp[q], (uint32_t)(uintptr_t)(ring + (q * 9 + 8) * 1024));
+      for (int q = 0; q < 4; ++q)
+        dma16(r.rb, r.orp[q], (uint32_t)(uintptr_t)(ring + (KV8 ? kRopeOff8 + q * 1024 : (q * 9 + 8) * 1024)));
     };
     auto prog_seg = [&](const ProgLoads& r, int sgm) __attribute__((always_inline)) {
+      if constexpr (KV8) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        dma16((const char*)r.nb + 128 * sgm, r.on[q], (uint32_t)(uintptr_t)(ring + (q * 9 + sgm) * 1024));
+        for (int q = 0; q < 4; ++q)
+          dma16(r.nb + 128 * sgm, r.on[q], (uint32_t)(uintptr_t)(ring + (q * 4 + sgm) * 1024));
+        dma16(r.scb + sgm * p.ks_sb, (uint32_t)((lane & 7) << 4), (uint32_t)(uintptr_t)(ring + kScaleOff8 + sgm * 1024));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          dma16(r.nb + 128 * sgm, r.on[q], (uint32_t)(uintptr_t)(ring + (q * 9 + sgm) * 1024));
+      }
     };
 
     // One pass over the segment's stages.  Returns true (uniformly across the workgroup)
@@ -896,7 +918,11 @@ void mla_splitkv_kernel(KParams p) {
       // O^T += V^T (P^T * s): the scales of V (per token and 128-dim block) multiply P^T, once
       // per block of eight dim tiles.  On the sequence's last stage the scales of rows past its
       // end are not data (their P is 0): they are replaced by 0 so that 0 * s stays 0.
-      auto pv_stage8 = [&](int kp, const float (&pvf)[HT][8], i32x2 (&vr)[DV]) __attribute__((always_inline)) {
+      // kProg: `seg(b)` after the last MFMA of 128-dim block b (its V^T codes and scales have
+      // all been read by then: each tile's codes are converted, and each block's scales taken,
+      // before the MFMAs that use them)
+      auto pv_stage8 = [&](int kp, const float (&pvf)[HT][8], i32x2 (&vr)[DV], const auto& seg)
+                           __attribute__((always_inline)) {
         const uint8_t LDS_AS* vb = v8_base(kp);
         const uint8_t LDS_AS* scb = ring + (kp % NSTAGE) * kSB + kScaleOff8 + 16 * g;
         const int left = L - (st_begin + kp) * kStageTok;
@@ -940,6 +966,9 @@ void mla_splitkv_kernel(KParams p) {
           if (new_block) make_pb((t + 1) >> 3, pbb_next);
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) o[t][ht] = mfma32<DT>(a_cur, pbb[ht], o[t][ht]);
+          if constexpr (kProg) {
+            if ((t & 7) == 7) seg(t >> 3);
+          }
           asm volatile("" ::"v"(a_prev));
           if ((t & 7) == 0 && t > 0) {
 #pragma unroll
@@ -968,7 +997,7 @@ void mla_splitkv_kernel(KParams p) {
         // kProg after the first own stage: the stage came in the order rope, segment 0, ..,
         // segment 7 (four loads each), so QK starts once the rope and segment 0 have landed
         // and waits for segment s only before its first fragment read (prog_wait)
-        constexpr bool kProgWait = kProg && MODE != kPassRowMax;
+        constexpr bool kProgWait = kProg && !KV8 && MODE != kPassRowMax;
         const bool prog_wait = kProgWait && j > 0;  // uniform
         if (prog_wait) {
           wait_vmcnt<28>();
@@ -1262,7 +1291,9 @@ void mla_splitkv_kernel(KParams p) {
         }
 
         if constexpr (kInl8) {
-          pv_stage8(k, pvf, vr);
+          pv_stage8(k, pvf, vr, [&](int blk) __attribute__((always_inline)) {
+            if (prog_next) prog_seg(prog, blk);
+          });
         } else if constexpr (kProg) {
           pv_stage(k, pb, vf, std::true_type{}, [&](int sgm) __attribute__((always_inline)) {
             if (prog_next) prog_seg(prog, sgm);
