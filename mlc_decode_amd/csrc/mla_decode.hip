@@ -562,7 +562,7 @@ void mla_splitkv_kernel(KParams p) {
   // wave split, dense 16-bit cache: a wave refills its slot with its next own stage while it
   // still computes the current one (rope blocks after QK, each 64-dim latent segment once PV
   // has read it), instead of in one burst after PV
-  constexpr bool kProg = WS && !SPARSE;
+  constexpr bool kProg = WS && !(SPARSE && KV8);
   __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[kSmem + (kDeq ? kStageBytes : 0)];
   // wave-split merge words: (row max, row sum of rounded P, row sum of fp32 P) per wave and row
   __shared__ float merge_sh[WS ? NW : 1][3][16];
@@ -748,16 +748,35 @@ void mla_splitkv_kernel(KParams p) {
     // blocks of latent segment s (block q*9 + s: rows 8q .. 8q+7, chunks 8s .. 8s+7)
     // fp8 cache (KV8, paged only): the loads of issue_stage8<1>, the latent in four 128-dim
     // blocks (prog_seg(s): block s of the four row groups and the stage's 32 scales of block s)
+    // sparse (bf16/fp16): each of the lane's four token rows has its own address (sn, sr)
     struct ProgLoads {
       const char* nb;
       const uint16_t* rb;
       const float* scb;
       uint32_t on[4], orp[4];
+      const char* sn[SPARSE ? 4 : 1];
+      const char* sr[SPARSE ? 4 : 1];
     };
     auto prog_prepare = [&](int k) __attribute__((always_inline)) {
       ProgLoads r;
       r.scb = nullptr;
       const int st = st_begin + k;
+      if constexpr (SPARSE) {  // as issue_stage_sparse<1>
+        const int valid_rows = (L - st * kStageTok) < kStageTok ? L - st * kStageTok : kStageTok;
+        const int32_t LDS_AS* idx_stage = (const int32_t LDS_AS*)idx_sh + k * kStageTok;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int rr = 8 * q + (lane >> 3);
+          const int t = rr < valid_rows ? rr : valid_rows - 1;
+          int64_t idx = idx_stage[t];
+          if (idx < 0 || idx >= p.pool_tokens) idx = 0;
+          const int64_t pg = idx >> 6, rw = idx & 63;
+          const uint32_t cl = (uint32_t)(((lane & 7) ^ stage_swz(((q & 1) << 3) | (lane >> 3))) << 4);
+          r.sn[q] = (const char*)(p.kv_nope + pg * p.kv_sp + rw * p.kv_st) + cl;
+          r.sr[q] = (const char*)(p.kv_rope + pg * p.kr_sp + rw * p.kr_st) + cl;
+        }
+        return r;
+      }
       if (paged) {
         const int pidx = st >> 1;
         if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
@@ -792,12 +811,21 @@ void mla_splitkv_kernel(KParams p) {
       return r;
     };
     auto prog_rope = [&](const ProgLoads& r) __attribute__((always_inline)) {
+      if constexpr (SPARSE) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dma16_lane(r.sr[q], (uint32_t)(uintptr_t)(ring + (q * 9 + 8) * 1024));
+        return;
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         dma16(r.rb, r.orp[q], (uint32_t)(uintptr_t)(ring + (KV8 ? kRopeOff8 + q * 1024 : (q * 9 + 8) * 1024)));
     };
     auto prog_seg = [&](const ProgLoads& r, int sgm) __attribute__((always_inline)) {
-      if constexpr (KV8) {
+      if constexpr (SPARSE) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          dma16_lane(r.sn[q] + 128 * sgm, (uint32_t)(uintptr_t)(ring + (q * 9 + sgm) * 1024));
+      } else if constexpr (KV8) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           dma16(r.nb + 128 * sgm, r.on[q], (uint32_t)(uintptr_t)(ring + (q * 4 + sgm) * 1024));
