@@ -2446,9 +2446,122 @@ __device__ __forceinline__ float merge_few_splits(const uint16_t* __restrict__ w
   return lse2;
 }
 
-// One wave per (sequence, row).
-template <int DT, typename PT, bool SCALED>
-__global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__ ws_o,
+// merge_splits_wave for a row of at most kDeepSplits 16-bit partials, by four waves that each
+// take one 128-dim quarter q of the row (lane l: dims 128 q + 2 l, +1), so a long merge runs on
+// four CUs instead of one.  A wave keeps kQueue quarter rows in flight in a register queue: the
+// loop, unrolled by kQueue, consumes split k from queue slot k % kQueue and reloads that slot
+// with split k + kQueue (an index past the last split is clamped to it), so consuming a slot
+// waits only for that slot's load.  The loop is issue-bound (one wave per SIMD; the queue depth
+// does not matter between 16 and 32), so a block whose splits are all live runs without the
+// per-split zeroing of surplus rows that the last block needs.  The lse of all splits (lane l
+// holds splits l, l + 64, ..) and the quarter's chunk scale come first; the weight of split k
+// times that scale is formed once, into kw[k] (0 past the last split).  Arithmetic per output
+// element is merge_splits_wave's operation for operation (the same per-lane order of the max
+// and the sum, the same butterfly, the same product w * s and fma chain in split order): the
+// result is bit-identical.  (An LDS-DMA ring in place of the queue was no faster.)
+constexpr int kDeepSplits = 256;
+constexpr int kQueue = 32;
+constexpr int kDeepLds = (kDeepSplits + kQueue) * 4;  // kw
+template <int DT, bool SCALED>
+__device__ __forceinline__ float merge_many_splits(const uint16_t* __restrict__ ws_o, const float* __restrict__ ws_scale,
+                                                   const float* __restrict__ ws_lse, int base, int n, int rows,
+                                                   int row, int q, int lane, char* smem, float (&acc)[2]) {
+  static_assert(kDeepSplits % 64 == 0 && kQueue <= 63 && kQueue % 4 == 0 && kQueue <= 64, "queue shape");
+  constexpr int LDT = SCALED ? MLA_DTYPE_F16 : DT;
+  constexpr int kL = kDeepSplits / 64;
+  float* kw = (float*)smem;
+  // split k's quarter row: a uniform base plus the lane's 4 bytes (offsets fit 32 bits: at most
+  // kDeepSplits splits of at most 2^16 rows of 1 KiB)
+  const char* row0 = (const char*)(ws_o + ((int64_t)base * rows + row) * kDV + 128 * q);
+  const uint32_t split_bytes = (uint32_t)rows * kDV * 2;
+  const float* lp = ws_lse + (int64_t)base * rows + row;
+  const int last = n - 1;
+  const uint32_t last_off = (uint32_t)last * split_bytes;
+  uint32_t next_off = 0;  // the next split to load, clamped to the last
+  auto load_next = [&]() __attribute__((always_inline)) {
+    const uint32_t v = *(const uint32_t*)(row0 + next_off + lane * 4);
+    next_off = next_off + split_bytes < last_off ? next_off + split_bytes : last_off;
+    return v;
+  };
+
+  float lv[kL], sc[kL];
+#pragma unroll
+  for (int c = 0; c < kL; ++c) {
+    const int k = c * 64 + lane;
+    const int kc = k < last ? k : last;
+    const float l = lp[(int64_t)kc * rows];
+    lv[c] = k < n ? l : -INFINITY;
+    if constexpr (SCALED) sc[c] = ws_scale[((int64_t)(base + kc) * rows + row) * 4 + q];
+  }
+  uint32_t qv[kQueue];
+#pragma unroll
+  for (int u = 0; u < kQueue; ++u) qv[u] = load_next();
+
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kL; ++c)
+    if (c * 64 + lane < n) mx = fmaxf(mx, lv[c]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  float sum = 0.f;
+  if (mx != -INFINITY)
+#pragma unroll
+    for (int c = 0; c < kL; ++c)
+      if (c * 64 + lane < n) sum += fast_exp2(lv[c] - mx);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const float lse2 = sum > 0.f ? mx + __log2f(sum) : -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kL; ++c) {
+    const int k = c * 64 + lane;
+    float w = 0.f;
+    if (k < n && lse2 != -INFINITY) w = fast_exp2(lv[c] - lse2);
+    kw[k] = SCALED ? w * sc[c] : w;
+  }
+  if (lane < kQueue) kw[kDeepSplits + lane] = 0.f;
+  __builtin_amdgcn_wave_barrier();
+
+  acc[0] = acc[1] = 0.f;
+  auto block = [&](int k0, auto tail) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u4 = 0; u4 < kQueue; u4 += 4) {
+      const f32x4 w4 = *(const f32x4*)&kw[k0 + u4];
+#pragma unroll
+      for (int u = u4; u < u4 + 4; ++u) {
+        // in the last block a row past the last split is zeroed: acc + 0 * 0 = acc exactly
+        // (acc is never -0)
+        const uint32_t v = (decltype(tail)::value && k0 + u >= n) ? 0u : qv[u];
+        float x0, x1;
+        if constexpr (LDT == MLA_DTYPE_BF16) {
+          x0 = __builtin_bit_cast(float, v << 16);
+          x1 = __builtin_bit_cast(float, v & 0xffff0000u);
+        } else {
+          const f16x2 h = __builtin_bit_cast(f16x2, v);
+          x0 = (float)h[0];
+          x1 = (float)h[1];
+        }
+        acc[0] += w4[u - u4] * x0;
+        acc[1] += w4[u - u4] * x1;
+        qv[u] = load_next();
+      }
+    }
+  };
+  for (int k0 = 0; k0 < n; k0 += kQueue) {
+    if (k0 + kQueue <= n)  // uniform
+      block(k0, std::false_type{});
+    else
+      block(k0, std::true_type{});
+  }
+  return lse2;
+}
+
+// One wave per (sequence, row).  DEEP (chosen by the host when the batch is small next to the
+// part count, so sequences have many splits and the grid is small): one wave per workgroup and
+// grid.z = 4, the quarter of the row the wave merges when the row has kFewSplits < n <=
+// kDeepSplits splits (merge_many_splits); other rows are merged whole by quarter 0.  Otherwise
+// four waves per workgroup, for large batches of rows with few splits each.
+template <int DT, typename PT, bool SCALED, bool DEEP = false>
+__global__ __launch_bounds__(DEEP ? 64 : 256) void mla_combine_kernel(const PT* __restrict__ ws_o,
                                                           const float* __restrict__ ws_scale,
                                                           const float* __restrict__ ws_lse,
                                                           const int32_t* __restrict__ splits,
@@ -2457,31 +2570,45 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const PT* __restrict__
                                                           int64_t o_sb, int64_t o_ss, int64_t o_sh,
                                                           float* __restrict__ lse_out,
                                                           int copy_single) {
-  __shared__ float w_sh[4][64];
+  constexpr int W = DEEP ? 1 : 4;  // waves (rows) per workgroup
+  __shared__ __attribute__((aligned(16))) char smem[DEEP ? kDeepLds : W * 64 * 4];
+  float* w_sh = (float*)smem + 64 * (threadIdx.x >> 6);  // the wave's 64 weights (merge_splits_wave)
   const int b = blockIdx.x;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.y * 4 + wave;
+  const int row = blockIdx.y * W + wave;
   if (row >= rows) return;
   const int base = splits[b];
   const int n = splits[b + 1] - base;
   if (n < 1 || (n == 1 && !copy_single)) return;
+  const int s = row / heads;
+  const int h = row - s * heads;
+  uint16_t* dst = out + b * o_sb + s * o_ss + h * o_sh;
+  float* lse_dst = lse_out != nullptr ? lse_out + ((int64_t)b * heads + h) * s_q + s : nullptr;
+  if constexpr (DEEP && std::is_same<PT, uint16_t>::value) {
+    const int q = blockIdx.z;
+    if (n > kFewSplits && n <= kDeepSplits) {  // uniform
+      float acc2[2];
+      const float lse2 = merge_many_splits<DT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, q, lane, smem, acc2);
+      *(uint32_t*)(dst + 128 * q + 2 * lane) = pack2<DT>(acc2[0], acc2[1]);
+      if (q == 0 && lane == 0 && lse_dst != nullptr) *lse_dst = lse2 * kLn2;
+      return;
+    }
+    if (q != 0) return;
+  }
   float acc[8];
   float lse2;
   if constexpr (std::is_same<PT, uint16_t>::value) {
     if (n <= kFewSplits)  // uniform
       lse2 = merge_few_splits<DT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane, acc);
     else
-      lse2 = merge_splits_wave<DT, PT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane, w_sh[wave], acc);
+      lse2 = merge_splits_wave<DT, PT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane, w_sh, acc);
   } else {
-    lse2 = merge_splits_wave<DT, PT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane, w_sh[wave], acc);
+    lse2 = merge_splits_wave<DT, PT, SCALED>(ws_o, ws_scale, ws_lse, base, n, rows, row, lane, w_sh, acc);
   }
-  const int s = row / heads;
-  const int h = row - s * heads;
-  uint16_t* dst = out + b * o_sb + s * o_ss + h * o_sh + lane * 8;
-  *(i32x4*)dst = i32x4{(int)pack2<DT>(acc[0], acc[1]), (int)pack2<DT>(acc[2], acc[3]),
-                       (int)pack2<DT>(acc[4], acc[5]), (int)pack2<DT>(acc[6], acc[7])};
-  if (lane == 0 && lse_out != nullptr) lse_out[((int64_t)b * heads + h) * s_q + s] = lse2 * kLn2;
+  *(i32x4*)(dst + lane * 8) = i32x4{(int)pack2<DT>(acc[0], acc[1]), (int)pack2<DT>(acc[2], acc[3]),
+                                    (int)pack2<DT>(acc[4], acc[5]), (int)pack2<DT>(acc[6], acc[7])};
+  if (lane == 0 && lse_dst != nullptr) *lse_dst = lse2 * kLn2;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -3325,15 +3452,20 @@ mla::KParams make_params(const mla_decode_args* a) {
 // mla_merge_partials, or the unscaled 16-bit rows of mla_launch (PT = uint16_t).
 template <typename PT, bool SCALED = false>
 int launch_combine(const mla::KParams& k, const PT* part_o, int dtype, int copy_single, hipStream_t st) {
-  dim3 grid(k.batch, (k.rows + 3) / 4);
-  if (dtype == MLA_DTYPE_BF16)
-    hipLaunchKernelGGL((mla::mla_combine_kernel<MLA_DTYPE_BF16, PT, SCALED>), grid, dim3(256), 0, st, part_o,
-                       k.ws_scale, k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
-                       k.lse, copy_single);
-  else
-    hipLaunchKernelGGL((mla::mla_combine_kernel<MLA_DTYPE_F16, PT, SCALED>), grid, dim3(256), 0, st, part_o,
-                       k.ws_scale, k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh,
-                       k.lse, copy_single);
+  // many splits per sequence on average: a small grid of long merges, each row split in four
+  // one-wave workgroups (dim quarters) so it runs on four CUs
+  const bool deep = std::is_same<PT, uint16_t>::value && k.num_parts >= 16 * k.batch;
+  const int W = deep ? 1 : 4;
+  const dim3 grid(k.batch, (k.rows + W - 1) / W, deep ? 4 : 1);
+#define MLA_COMBINE(D, DP)                                                                                      \
+  hipLaunchKernelGGL((mla::mla_combine_kernel<D, PT, SCALED, DP>), grid, dim3(64 * W), 0, st, part_o, k.ws_scale, \
+                     k.ws_lse, k.splits, k.rows, k.heads, k.s_q, k.out, k.o_sb, k.o_ss, k.o_sh, k.lse, copy_single)
+  if (dtype == MLA_DTYPE_BF16) {
+    if (deep) MLA_COMBINE(MLA_DTYPE_BF16, true); else MLA_COMBINE(MLA_DTYPE_BF16, false);
+  } else {
+    if (deep) MLA_COMBINE(MLA_DTYPE_F16, true); else MLA_COMBINE(MLA_DTYPE_F16, false);
+  }
+#undef MLA_COMBINE
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MLA_ERR_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
   return MLA_OK;

@@ -46,8 +46,10 @@ def check_close(got, ref, atol, what):
         assert cos >= COS_MIN, f"{what}: cosine {cos}"
 
 
+# forced 12: 60 parts for 5 sequences, the combine's 2-groups-of-4 merge; forced 40: 200 parts,
+# its 3-groups-of-16 merge (both bit-identical to the fused merge, checked below)
 @pytest.mark.parametrize("H,s_q", [(16, 1), (64, 1), (128, 1), (128, 2)])
-@pytest.mark.parametrize("forced", [0, 1, 3])
+@pytest.mark.parametrize("forced", [0, 1, 3, 12, 40])
 def test_absorb_matches_reference(gpu, H, s_q, forced):
     cfg = small_cfg(f"absorb_h{H}", 5, s_q, H, [0, 1, 100, 700, 3000])
     inp = make_inputs(cfg, seed=H + forced)

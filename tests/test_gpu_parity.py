@@ -231,6 +231,23 @@ def test_multi_split_outputs_in_2_4(gpu, H):
         assert_parity(out, lse, ref_o, ref_l, f"band H={H} ns={ns}")
 
 
+@pytest.mark.parametrize("H,dtype", [(16, torch.bfloat16), (16, torch.float16), (128, torch.bfloat16)])
+def test_many_splits_per_sequence(gpu, H, dtype):
+    """Sequences split 9 to 300 ways, against the oracle: the combine's prefetching merges (groups
+    of partial rows in flight, surplus reads past the last split zeroed; 2 groups of 4 when the
+    batch is large next to the part count, 3 groups of 16 when it is small), every count leaving
+    a partial last group, and the plain merge past 256 splits.  The short sequence has fewer
+    pages than splits, so many of its splits are empty (lse = -inf)."""
+    cfg = small_cfg(f"many_h{H}", 2, 1, H, [16384, 4001], dtype)
+    inp = make_inputs(cfg, seed=40 + H)
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                  inp.sm_scale, True)
+    for ns in (None, 9, 12, 40, 200, 256, 300):
+        say(f"many splits H={H} dtype={dtype} num_splits={ns}")
+        out, lse = run_paged(inp, gpu, ns)
+        assert_parity(out, lse, ref_o, ref_l, f"many splits H={H} ns={ns}")
+
+
 def _handmade_runner():
     """The library bound exactly as the reference binds its handmade kernel
     (handmade/mla_handmade.py:97-107): CDLL, argtypes [c_void_p] * 7 + [c_int], restype None."""
