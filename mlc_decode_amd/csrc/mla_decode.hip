@@ -2645,6 +2645,7 @@ struct AbsorbParams {
   uint16_t* v;           // [M, H, kVDim]
   float* lse;            // [B, H, s_q] natural log, or null
   int32_t m_rows, s_q, heads, rows;
+  int32_t premerged;     // 1: the combine kernel already wrote every row to `out` (and its lse)
 };
 
 template <int DT>
@@ -2684,6 +2685,7 @@ __global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams
       const int row = s * a.heads + h;
       const int base = a.splits[b];
       n[i] = a.splits[b + 1] - base;
+      if (a.premerged && n[i] > 1) n[i] = 1;  // the merged row is in `out`, its lse written
       if (n[i] == 1) {
         src1[i] = a.out + b * a.o_sb + s * a.o_ss + h * a.o_sh + lane * 8;
       } else {
@@ -3450,11 +3452,13 @@ mla::KParams make_params(const mla_decode_args* a) {
 
 // Partials are the decode workspace's scaled fp16 rows (SCALED), the caller's fp32 rows of
 // mla_merge_partials, or the unscaled 16-bit rows of mla_launch (PT = uint16_t).
+// Many splits per sequence on average: a small grid of long merges, which the combine kernel's
+// DEEP form runs with each row split in four one-wave workgroups (dim quarters).
+bool combine_is_deep(const mla::KParams& k) { return k.num_parts >= 16 * k.batch; }
+
 template <typename PT, bool SCALED = false>
 int launch_combine(const mla::KParams& k, const PT* part_o, int dtype, int copy_single, hipStream_t st) {
-  // many splits per sequence on average: a small grid of long merges, each row split in four
-  // one-wave workgroups (dim quarters) so it runs on four CUs
-  const bool deep = std::is_same<PT, uint16_t>::value && k.num_parts >= 16 * k.batch;
+  const bool deep = std::is_same<PT, uint16_t>::value && combine_is_deep(k);
   const int W = deep ? 1 : 4;
   const dim3 grid(k.batch, (k.rows + W - 1) / W, deep ? 4 : 1);
 #define MLA_COMBINE(D, DP)                                                                                      \
@@ -3648,6 +3652,14 @@ int mla_combine_absorb(const mla_decode_args* args, const void* w_uv_blk, void* 
   a.s_q = kp.s_q;
   a.heads = kp.heads;
   a.rows = kp.rows;
+  if (combine_is_deep(kp)) {
+    // long merges: the combine kernel's DEEP form writes the merged rows (bf16/fp16, as the
+    // fused merge rounds them into LDS) and their lse, and the projection reads every row from
+    // `out`; v is bit-identical to the fused merge's
+    const int rc2 = launch_combine<uint16_t, true>(kp, kp.ws_o, args->dtype, 0, (hipStream_t)stream);
+    if (rc2 != MLA_OK) return rc2;
+    a.premerged = 1;
+  }
   const dim3 grid(kp.heads, (a.m_rows + mla::kAbsRows - 1) / mla::kAbsRows);
   if (args->dtype == MLA_DTYPE_BF16)
     hipLaunchKernelGGL(mla::mla_combine_absorb_kernel<MLA_DTYPE_BF16>, grid, dim3(256), 0, (hipStream_t)stream, a);

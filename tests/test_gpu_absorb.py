@@ -46,8 +46,9 @@ def check_close(got, ref, atol, what):
         assert cos >= COS_MIN, f"{what}: cosine {cos}"
 
 
-# forced 12: 60 parts for 5 sequences, the combine's 2-groups-of-4 merge; forced 40: 200 parts,
-# its 3-groups-of-16 merge (both bit-identical to the fused merge, checked below)
+# forced 12: 60 parts for 5 sequences, merged in the fused kernel's prologue; forced 40: 200
+# parts (at least 16 per sequence), merged first by the combine kernel's dim-quarter form and
+# read back by the projection (v bit-identical either way, checked below)
 @pytest.mark.parametrize("H,s_q", [(16, 1), (64, 1), (128, 1), (128, 2)])
 @pytest.mark.parametrize("forced", [0, 1, 3, 12, 40])
 def test_absorb_matches_reference(gpu, H, s_q, forced):
@@ -185,3 +186,26 @@ def test_absorb_sparse(gpu):
     ref_o, _ = R.decode_sparse(q.cpu(), kv.cpu(), idx.cpu(), 576 ** -0.5)
     ref_v = torch.einsum("bshk,hkn->bshn", ref_o, w_uv.float())
     check_close(v, ref_v, V_RTOL * ref_v.abs().max().item(), "v sparse")
+
+
+@pytest.mark.parametrize("H", [16, 128])
+def test_absorb_long_single_sequence(gpu, H):
+    """Batch 1 at 16K tokens under the default schedule (up to 256 splits of the one sequence):
+    the merge runs in the combine kernel's dim-quarter form and the projection reads the merged
+    rows; against the oracle and against the combine's own rows and lse."""
+    cfg = small_cfg(f"absorb_long_h{H}", 1, 1, H, [16384])
+    inp = make_inputs(cfg, seed=60 + H)
+    w_uv, _ = weights(H, torch.bfloat16, 60 + H)
+    d = inp.to("cuda")
+    say(f"absorb long single sequence H={H}")
+    sched, splits = get_mla_metadata(d.cache_seqlens, H, 1)
+    assert splits[-1].item() > 64  # a long merge
+    v, lse = mla_decode_absorbed(d.q, d.kv_cache, d.block_table, d.cache_seqlens, sched, splits,
+                                 prepare_w_uv(w_uv.cuda()), softmax_scale=inp.sm_scale, causal=True)
+    out, lse2 = flash_mla_with_kvcache(d.q, d.kv_cache, d.block_table, d.cache_seqlens, 512, sched, splits,
+                                       softmax_scale=inp.sm_scale, causal=True)
+    torch.cuda.synchronize()
+    _fused_equals_combine(v, lse, out, lse2, w_uv, f"long H={H}")
+    ref_o, _ = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens, inp.sm_scale, True)
+    ref_v = torch.einsum("bshk,hkn->bshn", ref_o, w_uv.float())
+    check_close(v, ref_v, V_RTOL * ref_v.abs().max().item(), f"v long H={H}")
