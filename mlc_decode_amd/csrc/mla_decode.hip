@@ -2629,9 +2629,11 @@ __global__ __launch_bounds__(DEEP ? 64 : 256) void mla_combine_kernel(const PT* 
 //     weights, the same fma chain in split order;
 //  3. the wave's W_UV slab (32 columns, 128 registers) is loaded in one round trip and 2 MFMA
 //     tiles form the 16 x kVDim product.
-// At most 168 registers: three workgroups per CU.  (Measured alternatives: loading W_UV before
-// the merge, and 32-row workgroups of 8 waves that preload their 16-column slabs, were no
-// faster; the [h][n][k] layout, 16 half-lines per load, cost 3 us more at 128 heads x 64 rows.)
+// At most 256 registers (178 used): two workgroups per CU.  At three (168 registers) the
+// compiler spilled 28 of them to scratch and the kernel ran 4-21% slower.  (Measured
+// alternatives: loading W_UV before the merge, and 32-row workgroups of 8 waves that preload
+// their 16-column slabs, were no faster; the [h][n][k] layout, 16 half-lines per load, cost
+// 3 us more at 128 heads x 64 rows.)
 constexpr int kVDim = 128;
 constexpr int kAbsRows = 16;
 struct AbsorbParams {
@@ -2649,7 +2651,7 @@ struct AbsorbParams {
 };
 
 template <int DT>
-__global__ __launch_bounds__(256, 3) void mla_combine_absorb_kernel(AbsorbParams a) {
+__global__ __launch_bounds__(256, 2) void mla_combine_absorb_kernel(AbsorbParams a) {
   constexpr int RT = kAbsRows;     // rows per workgroup
   constexpr int kPitch = kDV + 8;  // 16-bit elements; 1040-byte rows keep the A reads conflict-free
   constexpr int R = RT / 4;        // rows merged by one wave
