@@ -2460,6 +2460,7 @@ __device__ __forceinline__ float merge_few_splits(const uint16_t* __restrict__ w
 // and the sum, the same butterfly, the same product w * s and fma chain in split order): the
 // result is bit-identical.  (An LDS-DMA ring in place of the queue was no faster.)
 constexpr int kDeepSplits = 256;
+constexpr int kDeepMaxRows = 16384;  // kDeepSplits * kDeepMaxRows KiB = 2^32 bytes
 constexpr int kQueue = 32;
 constexpr int kDeepLds = (kDeepSplits + kQueue) * 4;  // kw
 template <int DT, bool SCALED>
@@ -2470,8 +2471,10 @@ __device__ __forceinline__ float merge_many_splits(const uint16_t* __restrict__ 
   constexpr int LDT = SCALED ? MLA_DTYPE_F16 : DT;
   constexpr int kL = kDeepSplits / 64;
   float* kw = (float*)smem;
-  // split k's quarter row: a uniform base plus the lane's 4 bytes (offsets fit 32 bits: at most
-  // kDeepSplits splits of at most 2^16 rows of 1 KiB)
+  // split k's quarter row: a uniform base plus the lane's 4 bytes.  Offsets are 32-bit: the host
+  // takes this path only for rows <= kDeepMaxRows, so the last split's offset, at most
+  // (kDeepSplits - 1) * rows KiB, stays below 2^32 (a surplus load's offset may wrap, to an
+  // earlier split of the same row, and is consumed as zeros)
   const char* row0 = (const char*)(ws_o + ((int64_t)base * rows + row) * kDV + 128 * q);
   const uint32_t split_bytes = (uint32_t)rows * kDV * 2;
   const float* lp = ws_lse + (int64_t)base * rows + row;
@@ -3456,7 +3459,9 @@ mla::KParams make_params(const mla_decode_args* a) {
 // mla_merge_partials, or the unscaled 16-bit rows of mla_launch (PT = uint16_t).
 // Many splits per sequence on average: a small grid of long merges, which the combine kernel's
 // DEEP form runs with each row split in four one-wave workgroups (dim quarters).
-bool combine_is_deep(const mla::KParams& k) { return k.num_parts >= 16 * k.batch; }
+bool combine_is_deep(const mla::KParams& k) {
+  return k.num_parts >= 16 * k.batch && k.rows <= mla::kDeepMaxRows;
+}
 
 template <typename PT, bool SCALED = false>
 int launch_combine(const mla::KParams& k, const PT* part_o, int dtype, int copy_single, hipStream_t st) {
