@@ -2661,6 +2661,9 @@ __global__ __launch_bounds__(256, 2) void mla_combine_absorb_kernel(AbsorbParams
   constexpr int NT = 2;            // 16-column MFMA tiles per wave
   constexpr int KS = kDV / 32;     // MFMA k-steps
   constexpr int kPF = 2;           // partial rows per row loaded in one round trip
+  // a group of kPF splits must not cross a 64-split weight window (w_sh holds one window);
+  // 4 spills 61 registers at this launch bound
+  static_assert(64 % kPF == 0, "kPF divides the weight window");
   __shared__ __attribute__((aligned(16))) uint16_t a_sh[RT * kPitch];
   __shared__ float w_sh[RT][64];
   const int h = blockIdx.x;
