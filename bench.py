@@ -58,6 +58,8 @@ def parse():
                     help="skip the stream probe (profiling runs: keeps its copies out of the trace)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain MIB-MiB device copy 3x (scale for FETCH/WRITE_SIZE counters)")
+    ap.add_argument("--windows", type=int, default=5,
+                    help="timing windows of --steps calls each; every figure is their median")
     return ap.parse_args()
 
 
@@ -75,6 +77,22 @@ def cpu_model() -> str:
 def time_gpu(fn, steps, warmup, stream):
     from mlc_decode_amd.timing import time_gpu as _time_gpu
     return _time_gpu(fn, steps, warmup, stream)
+
+
+WINDOWS = 5  # timing windows per figure; the median is reported (set by --windows)
+
+
+def time_windows(fn, steps, warmup, stream, windows=None):
+    """ms per call in each of ``windows`` windows of exactly ``steps`` calls (HIP events on
+    ``stream``, a synchronisation on both sides of every window); ``warmup`` untimed calls
+    before the first."""
+    n = WINDOWS if windows is None else windows
+    return [time_gpu(fn, steps, warmup if i == 0 else 0, stream) for i in range(n)]
+
+
+def median(xs):
+    import statistics
+    return statistics.median(xs)
 
 
 def settle_clocks(fn, stream, seconds=0.25):
@@ -142,6 +160,55 @@ def stream_probe(reps=20):
     return res
 
 
+PEAK_SCLK_MHZ = 2400.0  # MI355X peak engine clock, at which the 2.5 PFLOP/s dense bf16 figure holds
+
+
+def mfma_probe(iters=100000):
+    """Dense bf16 MFMA rate the device sustains (eight independent 16x16x32 chains per wave,
+    two waves per SIMD on every CU) and the shader clock measured during it (clock64 against
+    the wall clock): the MFMA counterpart of the stream probe, and the clock that scales the
+    spec peak (2.5 PFLOP/s at 2400 MHz) to this run."""
+    import ctypes
+    import statistics
+
+    import torch
+    from mlc_decode_amd.build import PROBE_PATH
+    lib = ctypes.CDLL(PROBE_PATH)
+    lib.mla_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.mla_probe_mfma.restype = ctypes.c_int
+    lib.mla_probe_wall_clock_khz.restype = ctypes.c_int
+    props = torch.cuda.get_device_properties(0)
+    wgs = 2 * props.multi_processor_count
+    sink = torch.empty(wgs * 256 * 4, dtype=torch.float32, device="cuda:0")
+    clocks = torch.zeros(wgs * 4, dtype=torch.int64, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    run = lambda n: lib.mla_probe_mfma(n, sink.data_ptr(), clocks.data_ptr(), wgs, stream.cuda_stream)  # noqa: E731
+    if run(iters // 10) != 0:
+        raise RuntimeError("mfma probe launch failed")
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(3):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        run(iters)
+        e.record(stream)
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    ms = statistics.median(times)
+    flops = wgs * 4 * iters * 8 * 2 * 16 * 16 * 32
+    c = clocks.view(wgs, 4).cpu().double()
+    wall_khz = lib.mla_probe_wall_clock_khz()
+    ratio = ((c[:, 2] - c[:, 0]) / (c[:, 3] - c[:, 1]).clamp(min=1)).median().item()
+    sclk = ratio * wall_khz / 1e3 if wall_khz > 0 else None
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"tflops": round(tflops, 1), "sclk_mhz": None if sclk is None else round(sclk, 1),
+            "wall_clock_khz": wall_khz,
+            "peak_at_clock_tflops": None if sclk is None else round(MFMA_PEAK_TFLOPS * sclk / PEAK_SCLK_MHZ, 1),
+            "probe": f"{wgs} workgroups x 4 waves x {iters} rounds of 8 independent v_mfma_f32_16x16x32_bf16, "
+                     "median of 3 launches"}
+
+
 FP8_TOKEN_BYTES = 512 + 64 * 2 + 4 * 4  # e4m3 latent codes, bf16 rope, four fp32 block scales
 
 
@@ -181,14 +248,16 @@ def measure(cfg_name, steps, warmup, kv_fp8=False, cold=True):
                                out=out, lse=lse)
 
     settle_clocks(call, stream)
-    ms_call = time_gpu(call, steps, warmup, stream)
+    win_call = time_windows(call, steps, warmup, stream)
+    ms_call = median(win_call)
     # the two kernels separately, launched through the C ABI on the same stream
-    ms_main = time_gpu(lambda: check("mla_splitkv_fwd", lib.mla_splitkv_fwd(ap, sp)),
-                       steps, warmup, stream)
-    ms_combine = time_gpu(lambda: check("mla_combine_fwd", lib.mla_combine_fwd(ap, sp)),
-                          steps, warmup, stream)
-    ms_meta = time_gpu(lambda: get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=forced),
-                       steps, warmup, stream)
+    win_main = time_windows(lambda: check("mla_splitkv_fwd", lib.mla_splitkv_fwd(ap, sp)),
+                            steps, warmup, stream)
+    ms_main = median(win_main)
+    ms_combine = median(time_windows(lambda: check("mla_combine_fwd", lib.mla_combine_fwd(ap, sp)),
+                                     steps, warmup, stream))
+    ms_meta = median(time_windows(lambda: get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=forced),
+                                  steps, warmup, stream))
 
     def end_to_end():  # the schedule computed in the call, then the decode on it
         sc, sp_ = get_mla_metadata(inp.cache_seqlens, s_q * H, 1, forced_splits=forced)
@@ -196,7 +265,7 @@ def measure(cfg_name, steps, warmup, kv_fp8=False, cold=True):
                                sc, sp_, softmax_scale=inp.sm_scale, causal=inp.causal,
                                out=out, lse=lse)
 
-    ms_e2e = time_gpu(end_to_end, steps, warmup, stream)
+    ms_e2e = median(time_windows(end_to_end, steps, warmup, stream))
     ms_cold = None if not cold else time_cold(call, max(10, min(steps, 40)), stream)
     ms_cold_dirty = None if not cold else time_cold(call, max(10, min(steps, 40)), stream, dirty=True)
     del keep
@@ -215,6 +284,7 @@ def measure(cfg_name, steps, warmup, kv_fp8=False, cold=True):
     call_frac = (nbytes / (ms_call * 1e-3) / 1e9 / HBM_PEAK_GBS if bound == "hbm"
                  else flops / (ms_call * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS)
     return dict(cfg=cfg, cpu_inp=cpu_inp, ms_call=ms_call, ms_main=ms_main, ms_combine=ms_combine,
+                windows_call=win_call, windows_main=win_main,
                 ms_meta=ms_meta, ms_e2e=ms_e2e, ms_cold=ms_cold, ms_cold_dirty=ms_cold_dirty,
                 nbytes=nbytes, flops=flops,
                 bound=bound, gbs=gbs, tflops=tflops, call_frac=call_frac,
@@ -446,7 +516,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    global WINDOWS
+    WINDOWS = max(1, args.windows)
     probe = None if args.no_probe else stream_probe()
+    mprobe = None if args.no_probe else mfma_probe()
     m = measure(args.config, args.steps, args.warmup, cold=not args.no_cold)
     cfg = m["cfg"]
     if args.all_configs:
@@ -454,7 +527,8 @@ def main():
         from mlc_decode_amd.api import kernel_variant
         record = {"device": torch.cuda.get_device_name(0), "arch": "gfx950",
                   "command": "python bench.py " + " ".join(sys.argv[1:]),
-                  "peaks": {"hbm_gbs": HBM_PEAK_GBS, "mfma_bf16_tflops": MFMA_PEAK_TFLOPS},
+                  "peaks": {"hbm_gbs": HBM_PEAK_GBS, "mfma_bf16_tflops": MFMA_PEAK_TFLOPS,
+                            "stream_probe_gbs": probe, "mfma_probe": mprobe},
                   "configs": {}}
         for name in ("C1", "C2", "C3", "C4", "C5"):
             mm = m if name == args.config else measure(name, max(20, args.steps // 4), 5, cold=not args.no_cold)
@@ -469,6 +543,9 @@ def main():
                      "call_frac": round(mm["call_frac"], 4),
                      "tbps": round(mm["gbs"] / 1e3, 3), "tflops": round(mm["tflops"], 1),
                      "bound": mm["bound"], "roofline_frac": round(frac, 4),
+                     "mfma_frac_of_clock_peak": (round(mm["tflops"] / mprobe["peak_at_clock_tflops"], 4)
+                                                 if mprobe and mprobe["peak_at_clock_tflops"] else None),
+                     "hbm_frac_of_measured_peak": round(mm["gbs"] / probe["best"], 4) if probe else None,
                      "parts": mm["parts"], "splits": mm["n_splits"]}
             print(json.dumps({"config": name, **entry}), file=sys.stderr, flush=True)
             record["configs"][name] = {
@@ -516,7 +593,18 @@ def main():
         "us_call_cold_dirty": None if m["ms_cold_dirty"] is None else round(m["ms_cold_dirty"] * 1e3, 3),
         "call_roofline_frac": round(m["call_frac"], 4),
         "stream_probe_gbs": probe,
-        "frac_of_measured_peak": (round(m["gbs"] / probe["best"], 4) if m["bound"] == "hbm" and probe else None),
+        "timing": f"median of {WINDOWS} windows of {args.steps} calls each",
+        "windows_us_call": [round(x * 1e3, 3) for x in m["windows_call"]],
+        "windows_us_main": [round(x * 1e3, 3) for x in m["windows_main"]],
+        "mfma_probe": mprobe,
+        # MFMA utilisation of the main kernel against the spec peak scaled to the measured clock
+        # (reported for every config; the binding fraction for the MFMA-bound ones)
+        "mfma_frac_of_clock_peak": (round(m["tflops"] / mprobe["peak_at_clock_tflops"], 4)
+                                    if mprobe and mprobe["peak_at_clock_tflops"] else None),
+        "mfma_frac_of_measured_peak": round(m["tflops"] / mprobe["tflops"], 4) if mprobe else None,
+        "frac_of_measured_peak": (round(m["gbs"] / probe["best"], 4) if m["bound"] == "hbm" and probe else
+                                  round(m["tflops"] / mprobe["tflops"], 4) if m["bound"] == "mfma" and mprobe
+                                  else None),
         "call_frac_of_measured_peak": (round(m["nbytes"] / (m["ms_call"] * 1e-3) / 1e9 / probe["best"], 4)
                                        if m["bound"] == "hbm" and probe else None),
         "roofline": {"bound": m["bound"], "achieved": round(achieved, 2), "peak": peak,

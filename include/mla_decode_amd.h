@@ -33,7 +33,9 @@
 extern "C" {
 #endif
 
-#define MLA_DECODE_AMD_VERSION 1
+/* 2: mla_decode_args gained block_table_width / table_reserved / status (a decode bounded by
+ * the block table's width). */
+#define MLA_DECODE_AMD_VERSION 2
 
 /* dtypes of q / kv / out */
 #define MLA_DTYPE_BF16 0
@@ -69,7 +71,8 @@ extern "C" {
  *
  * KV addressing:
  *   block_table != NULL (paged):  token t of sequence b lives in page
- *     p = block_table[b * block_table_stride + t / 64], row t % 64:
+ *     p = block_table[b * block_table_stride + t / 64], row t % 64 (t / 64 below
+ *     block_table_width; tokens past 64 * block_table_width are not read, see below):
  *     latent at kv_nope + p*kv_stride_page + (t%64)*kv_stride_tok
  *     rope   at kv_rope + p*kv_rope_stride_page + (t%64)*kv_rope_stride_tok
  *   block_table == NULL (contiguous, the reference's [B, L, 1, D] layout):
@@ -142,6 +145,16 @@ typedef struct mla_decode_args {
   const int32_t* indices;
   int32_t indices_stride;
   int32_t topk;
+
+  /* Paged mode: the number of valid columns of block_table (1 .. block_table_stride, at most
+   * 2^24).  A sequence needs pages_of(L) = ceil(L / 64) columns; a sequence whose
+   * cache_seqlens entry exceeds 64 * block_table_width is decoded over its first
+   * 64 * block_table_width tokens only, no column at or past the width is read, and *status is
+   * set to 1 (when status is non-NULL; the caller clears it).  Unused in contiguous and
+   * sparse mode. */
+  int32_t block_table_width;
+  int32_t table_reserved; /* must be 0 */
+  int32_t* status;        /* optional device int32, set to 1 on a length past the table */
 } mla_decode_args;
 
 /* Library version (MLA_DECODE_AMD_VERSION). */
@@ -297,7 +310,13 @@ void mla_launch(const void* Q, const void* Qpe, const void* KV, const void* Kpe,
  * Absorbed value projection after the split-KV pass (the step that consumes the decode's
  * output in an MLA layer; no counterpart in the reference): with the same args as the
  * preceding mla_splitkv_fwd, merge each (sequence, query, head) row's split partials (the
- * combine) and multiply it by that head's up-projection, without writing the merged latent row:
+ * combine) and multiply it by that head's up-projection.  For most shapes the merged latent
+ * row is formed on chip and never written; when the batch averages 16 or more parts per
+ * sequence (num_parts >= 16 * batch, s_q * heads_q <= 16384) the merge runs first as
+ * mla_combine_fwd does and writes every multi-split row and its lse into args->out, which the
+ * projection then reads.  So args->out is clobbered by this call and cannot hold other data
+ * between mla_splitkv_fwd and here (rows of single-split sequences are those the split-KV pass
+ * wrote there):
  *   v[b, s, h, n] = sum_k o[b, s, h, k] * W_UV[h][k][n],  k < 512, n < 128,
  * where w_uv_blk holds W_UV k-blocked by 32, w_uv_blk[h][kb][n][kk] = W_UV[h][32 kb + kk][n]
  * ([H, 16, 128, 32] contiguous in the query dtype, 16-byte aligned: each MFMA k-step of 16

@@ -97,6 +97,9 @@ class MlaDecodeArgs(ctypes.Structure):
         ("indices", _vp),
         ("indices_stride", _i32),
         ("topk", _i32),
+        ("block_table_width", _i32),
+        ("table_reserved", _i32),
+        ("status", _vp),
     ]
 
 

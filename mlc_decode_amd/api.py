@@ -57,8 +57,9 @@ def workspace(device: torch.device, nbytes: int, stream: Optional[torch.cuda.Str
     calls on one stream run in order and can share it, calls on different streams never do.
     A buffer, once handed out, is never freed (a HIP graph captured with its address may
     replay later): when a call needs more, the old buffer is kept alive until the process ends
-    and a larger one takes its place.  The returned slice's length is the byte count to pass
-    as ``workspace_bytes``.
+    and a larger one takes its place.  Sizes grow geometrically (``grown_workspace_size``), so
+    the retired buffers of a stream together hold less than its live one.  The returned
+    slice's length is the byte count to pass as ``workspace_bytes``.
     """
     nbytes = max(int(nbytes), 256)
     if stream is None:
@@ -68,12 +69,24 @@ def workspace(device: torch.device, nbytes: int, stream: Optional[torch.cuda.Str
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() - (-buf.data_ptr()) % 256 < nbytes:
+            size = grown_workspace_size(None if buf is None else buf.numel(), nbytes + 256)
             if buf is not None:
                 _retired.append(buf)
-            buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
             _workspaces[key] = buf
     off = (-buf.data_ptr()) % 256
     return buf[off:]
+
+
+def grown_workspace_size(current: Optional[int], need: int) -> int:
+    """Bytes of the buffer that replaces one of ``current`` bytes (None: no buffer yet) when a
+    call needs ``need``: the next power of two of at least ``need`` and twice ``current``.  Each
+    buffer is then at least twice its predecessor, so the buffers retired on the way to a
+    live one sum to less than it, whatever sequence of requests led there."""
+    size = 1 << max(int(need) - 1, 1).bit_length()
+    if current is not None:
+        size = max(size, 2 * int(current))
+    return size
 
 
 def num_parts_for(batch: int, s_q: int, heads_q: int, heads_k: int = 1, cu_count: int = 0) -> int:
@@ -197,9 +210,13 @@ def _split_kv(kv_cache) -> Tuple[torch.Tensor, torch.Tensor]:
 def make_decode_args(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tensor],
                      cache_seqlens: Optional[torch.Tensor], sched: torch.Tensor, splits: torch.Tensor,
                      sm_scale: float, causal: bool, out: Optional[torch.Tensor] = None,
-                     lse: Optional[torch.Tensor] = None, indices: Optional[torch.Tensor] = None):
+                     lse: Optional[torch.Tensor] = None, indices: Optional[torch.Tensor] = None,
+                     status: Optional[torch.Tensor] = None):
     """Validate a paged decode and fill the C ``mla_decode_args`` for it.
 
+    The decode reads no block-table column at or past ``block_table.shape[1]``: a sequence
+    whose ``cache_seqlens`` entry exceeds ``64 * block_table.shape[1]`` is decoded over the
+    tokens its row covers, and ``status[0]`` (int32, on the device, if given) is set to 1.
     Returns ``(args, out, lse, keep)``; ``keep`` holds the tensors the args point into and
     must stay alive while the args are used.
     """
@@ -246,6 +263,10 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tens
             raise ValueError("batch size of q, block_table, cache_seqlens and num_splits disagree")
     if q.stride(-1) != 1:
         raise ValueError("q must have unit stride in its last dim")
+    if status is not None:
+        _require_gpu(status, "status")
+        if status.dtype != torch.int32 or status.numel() < 1:
+            raise ValueError("status must be an int32 tensor of at least one element")
     if out is None:
         out = torch.empty(B, s_q, H, MLA_DIM_V, dtype=q.dtype, device=q.device)
     if lse is None:
@@ -285,7 +306,10 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tens
         a.kv_stride_batch = a.kv_rope_stride_batch = 0
     else:
         a.block_table = block_table.data_ptr()
-        a.block_table_stride = block_table.stride(0)
+        # one row: its stride is never used, and a view's may be anything
+        a.block_table_stride = block_table.stride(0) if B > 1 else block_table.shape[1]
+        a.block_table_width = block_table.shape[1]
+    a.status = status.data_ptr() if status is not None else None
     a.num_parts = num_parts
     a.cache_seqlens = seqlens.data_ptr() if seqlens is not None else None
     a.tile_sched = sched.data_ptr()
@@ -295,15 +319,22 @@ def make_decode_args(q: torch.Tensor, kv_cache, block_table: Optional[torch.Tens
     a.lse = lse.data_ptr()
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws.numel()
-    keep = (q, latent, rope, scale, block_table, seqlens, sched, splits, out, lse, ws, indices)
+    keep = (q, latent, rope, scale, block_table, seqlens, sched, splits, out, lse, ws, indices, status)
     return a, out, lse, keep
 
 
 def _decode(q, kv_cache, block_table, cache_seqlens, sched, splits, sm_scale, causal,
-            out=None, lse=None, indices=None):
+            out=None, lse=None, indices=None, status=None, single_split=False):
+    """One decode through the C ABI.  ``single_split``: the schedule is known to give every
+    sequence one split (forced ``num_splits = 1``), so the split-KV pass finishes every row and
+    the combine launch is skipped."""
     a, out, lse, keep = make_decode_args(q, kv_cache, block_table, cache_seqlens, sched, splits,
-                                         sm_scale, causal, out, lse, indices)
-    check("mla_decode_fwd", _lib.load().mla_decode_fwd(ctypes.byref(a), _stream_ptr(q.device)))
+                                         sm_scale, causal, out, lse, indices, status)
+    lib = _lib.load()
+    if single_split:
+        check("mla_splitkv_fwd", lib.mla_splitkv_fwd(ctypes.byref(a), _stream_ptr(q.device)))
+    else:
+        check("mla_decode_fwd", lib.mla_decode_fwd(ctypes.byref(a), _stream_ptr(q.device)))
     del keep
     return out, lse
 
@@ -313,7 +344,7 @@ def flash_mla_with_kvcache(q: torch.Tensor, k_cache, block_table: torch.Tensor,
                            tile_scheduler_metadata: torch.Tensor, num_splits: torch.Tensor,
                            softmax_scale: Optional[float] = None, causal: bool = False,
                            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
-                           indices: Optional[torch.Tensor] = None):
+                           indices: Optional[torch.Tensor] = None, status: Optional[torch.Tensor] = None):
     """Paged decode with a precomputed schedule -> ``(out [B,s_q,H,512], lse [B,H,s_q])``.
 
     Same call shape as the reference's use of FlashMLA (handmade/bench_metax_flashmla.py:33-35).
@@ -322,13 +353,16 @@ def flash_mla_with_kvcache(q: torch.Tensor, k_cache, block_table: torch.Tensor,
     cache names no key), ``block_table`` / ``cache_seqlens`` are not read and the schedule must
     come from ``get_mla_metadata(..., topk=topk)``.  No counterpart in the reference's Python
     path: MetaX FlashMLA ships such a kernel (docs/flashmla_metax_analysis.md:43).
+    No block-table column at or past ``block_table.shape[1]`` is read: a longer
+    ``cache_seqlens`` entry is cut to the table and sets ``status[0] = 1`` (``status``: an
+    int32 device tensor the caller clears, optional).
     """
     if head_dim_v != MLA_DIM_V:
         raise ValueError(f"head_dim_v must be {MLA_DIM_V}")
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** -0.5
     return _decode(q, k_cache, block_table, cache_seqlens, tile_scheduler_metadata, num_splits,
-                   softmax_scale, causal, out, lse, indices)
+                   softmax_scale, causal, out, lse, indices, status)
 
 
 def prepare_w_uv(w_uv: torch.Tensor) -> torch.Tensor:
@@ -381,12 +415,14 @@ def mla_decode_with_kvcache(q: torch.Tensor, kv_cache, block_table: torch.Tensor
                             cache_seqlens: torch.Tensor,
                             num_splits: Union[None, int, Tuple[torch.Tensor, torch.Tensor]] = None,
                             sm_scale: Optional[float] = None, causal: bool = True,
-                            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+                            out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+                            status: Optional[torch.Tensor] = None):
     """Schedule + decode in one call -> ``(out, lse)``.
 
     ``num_splits``: ``None`` = balanced schedule for this GPU; an ``int`` = cut every
-    sequence into that many page ranges (1 = the reference's serial baseline); or a
-    ``(tile_scheduler_metadata, num_splits)`` pair from :func:`get_mla_metadata`.
+    sequence into that many page ranges (1 = the reference's serial baseline: one launch,
+    no combine); or a ``(tile_scheduler_metadata, num_splits)`` pair from
+    :func:`get_mla_metadata`.  ``status`` as in :func:`flash_mla_with_kvcache`.
     """
     if sm_scale is None:
         sm_scale = MLA_DIM_QK ** -0.5
@@ -398,7 +434,11 @@ def mla_decode_with_kvcache(q: torch.Tensor, kv_cache, block_table: torch.Tensor
             raise ValueError("num_splits must be >= 1")
         sched, splits = get_mla_metadata(cache_seqlens, q.shape[1] * q.shape[2], 1,
                                          forced_splits=forced)
-    return _decode(q, kv_cache, block_table, cache_seqlens, sched, splits, sm_scale, causal, out, lse)
+        if forced == 1:
+            return _decode(q, kv_cache, block_table, cache_seqlens, sched, splits, sm_scale, causal,
+                           out, lse, status=status, single_split=True)
+    return _decode(q, kv_cache, block_table, cache_seqlens, sched, splits, sm_scale, causal, out, lse,
+                   status=status)
 
 
 def merge_partials(part_o: torch.Tensor, part_lse: torch.Tensor, num_splits: torch.Tensor,

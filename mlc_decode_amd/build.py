@@ -18,6 +18,9 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmla_decode_amd.so")
 SOURCES = [os.path.join(CSRC, "mla_decode.hip")]
+# bench.py's MFMA-rate and shader-clock probe (a measurement helper, not the decode's ABI)
+PROBE_PATH = os.path.join(LIB_DIR, "libmla_probe.so")
+PROBE_SOURCES = [os.path.join(CSRC, "mla_probe.hip")]
 ARCH = "gfx950"
 
 
@@ -29,9 +32,16 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile the library and return its path.  Always recompiles."""
+    """Compile the decode library and the probe library; return the decode library's path.
+    Always recompiles."""
+    _compile(SOURCES, LIB_PATH, verbose)
+    _compile(PROBE_SOURCES, PROBE_PATH, verbose)
+    return LIB_PATH
+
+
+def _compile(sources, target: str, verbose: bool) -> None:
     os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
+    tmp = target + ".tmp"
     cmd = [
         hipcc(),
         f"--offload-arch={ARCH}",
@@ -45,7 +55,7 @@ def build(verbose: bool = False) -> str:
         "-I", INCLUDE,
         "-I", CSRC,
         "-o", tmp,
-        *SOURCES,
+        *sources,
     ]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -56,8 +66,7 @@ def build(verbose: bool = False) -> str:
         for line in (proc.stdout + proc.stderr).splitlines():
             if noise not in line and line.strip():
                 print(line)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, target)
 
 
 if __name__ == "__main__":

@@ -75,6 +75,10 @@ struct KParams {
   const int32_t* block_table;
   int32_t bt_stride;
   int32_t num_blocks;
+  // paged: valid columns of the block table; a longer sequence is cut to 64 * bt_width tokens
+  // and raises *status (if non-NULL)
+  int32_t bt_width;
+  int32_t* status;
   const int32_t* seqlens;
   const int32_t* sched;
   const int32_t* splits;
@@ -513,6 +517,22 @@ __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
 
+// Sequence b's length as the kernels use it: negative lengths read as 0, and a paged sequence
+// longer than its block-table row (64 * bt_width tokens) is cut there, so no column past the
+// table's width is read; that raises the caller's status word (every lane stores the same 1).
+__device__ __forceinline__ int seq_len_bounded(const KParams& p, int b, bool paged) {
+  int L = p.seqlens[b];
+  L = L > 0 ? L : 0;
+  if (paged) {
+    const int cap = p.bt_width * kPageTokens;  // bt_width <= 2^24, checked by the host
+    if (L > cap) {  // uniform
+      L = cap;
+      if (p.status != nullptr) *p.status = 1;
+    }
+  }
+  return L;
+}
+
 // Waves per SIMD a variant is compiled for: four waves of one 16-row tile each with at most
 // a 2-stage ring fit 256 registers, so two workgroups share a CU; everything else takes the
 // whole register file (one wave per SIMD).
@@ -533,9 +553,9 @@ constexpr int waves_per_simd(int nw, int ht, int nstage, bool ws) {
 // block (bf16 queries and rope); K fragments are converted to bf16 with their scale on the way
 // from LDS to the MFMA, V^T fragments without it, and the scales of V are folded into P^T.
 // SPARSE: the keys of a sequence are the top-k pool tokens its index list names (s_q = 1).
+// (HIP's second launch bound is the minimum number of waves per SIMD, amdgpu_waves_per_eu.)
 template <int DT, int NW, int HT, int NSTAGE, bool WS, bool KV8, bool SPARSE = false>
-__global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW > 0
-                                          ? waves_per_simd(NW, HT, NSTAGE, WS) * 4 / NW : 1)
+__global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE, WS))
 void mla_splitkv_kernel(KParams p) {
   static_assert(NW == 1 || NW == 4, "one or four waves per workgroup");
   static_assert(!WS || NSTAGE == 1, "wave-split workgroups give each wave a one-stage slot");
@@ -631,7 +651,7 @@ void mla_splitkv_kernel(KParams p) {
 #pragma unroll 1
   for (; b < p.batch; ++b, page = 0, split = 0) {
     if (!(b < end_b || (b == end_b && page < end_page))) break;
-    const int L = SPARSE ? p.topk : (p.seqlens[b] > 0 ? p.seqlens[b] : 0);
+    const int L = SPARSE ? p.topk : seq_len_bounded(p, b, paged);
     const int np = pages_of(L);
     const int stop = (b == end_b) ? end_page : np;
     const int st_begin = 2 * page;
@@ -1634,7 +1654,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
 #pragma unroll 1
   for (; b < p.batch; ++b, page = 0, split = 0) {
     if (!(b < end_b || (b == end_b && page < end_page))) break;
-    const int L = p.seqlens[b] > 0 ? p.seqlens[b] : 0;
+    const int L = seq_len_bounded(p, b, p.block_table != nullptr);
     const int np = pages_of(L);
     const int stop = (b == end_b) ? end_page : np;
     const int st_begin = 2 * page;
@@ -3381,6 +3401,9 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
     if (a->kv_stride_page >= (int64_t(1) << 32) || a->kv_rope_stride_page >= (int64_t(1) << 32))
       return fail(MLA_ERR_UNSUPPORTED, "page strides must be below 2^32 elements");
     if (a->block_table_stride < 1) return fail(MLA_ERR_INVALID, "block_table_stride must be >= 1");
+    if (a->block_table_width < 1 || a->block_table_width > a->block_table_stride ||
+        a->block_table_width > (1 << 24))
+      return fail(MLA_ERR_INVALID, "block_table_width must be in [1, min(block_table_stride, 2^24)]");
     if (a->num_blocks < 1) return fail(MLA_ERR_INVALID, "num_blocks must be >= 1");
   } else {
     if (a->kv_stride_batch < 0 || a->kv_stride_batch % 8 || a->kv_rope_stride_batch < 0 ||
@@ -3393,6 +3416,8 @@ int validate(const mla_decode_args* a, int64_t* need_ws) {
   if (a->num_parts < 1) return fail(MLA_ERR_INVALID, "num_parts must be >= 1");
   if ((a->kv_format != MLA_KV_NATIVE && a->kv_format != MLA_KV_FP8_E4M3) || a->kv_reserved != 0)
     return fail(MLA_ERR_INVALID, "kv_format must be MLA_KV_NATIVE or MLA_KV_FP8_E4M3 (kv_reserved 0)");
+  if (a->table_reserved != 0) return fail(MLA_ERR_INVALID, "table_reserved must be 0");
+  if (a->status != nullptr && !aligned(a->status, 4)) return fail(MLA_ERR_INVALID, "status must be 4-byte aligned");
   if (a->indices) {
     if (a->s_q != 1) return fail(MLA_ERR_UNSUPPORTED, "the sparse decode takes s_q == 1");
     if (a->topk < 1 || a->topk > MLA_SPARSE_MAX_TOPK)
@@ -3436,6 +3461,8 @@ mla::KParams make_params(const mla_decode_args* a) {
   k.pool_tokens = (int64_t)a->num_blocks * mla::kPageTokens;
   k.block_table = a->block_table;
   k.bt_stride = a->block_table_stride;
+  k.bt_width = a->block_table_width;
+  k.status = a->status;
   k.num_blocks = a->num_blocks;
   k.seqlens = a->cache_seqlens;
   k.sched = a->tile_sched;

@@ -46,6 +46,7 @@ class MlaKernel:
         if not self.sm_scale > 0:
             raise ValueError("sm_scale must be > 0")
         self._state = {}  # device -> (seqlens, sched, num_splits)
+        self._prepared = None  # (key of the last call's tensors, its prepared C arguments)
 
     def __repr__(self) -> str:
         pol = "balanced" if self.splits is None else f"{self.splits} split(s)/sequence"
@@ -63,8 +64,17 @@ class MlaKernel:
             self._state[key] = st
         return st
 
-    def __call__(self, q: torch.Tensor, q_pe: torch.Tensor, kv: torch.Tensor, k_pe: torch.Tensor,
-                 output: Optional[torch.Tensor] = None):
+    @staticmethod
+    def _key(q, q_pe, kv, k_pe, output):
+        """Everything the prepared arguments depend on: pointers, shapes, strides, dtypes,
+        the device and torch's current stream on it."""
+        ts = (q, q_pe, kv, k_pe)
+        return (tuple((t.data_ptr(), t.shape, t.stride(), t.dtype, t.device) for t in ts),
+                None if output is None else (output.data_ptr(), output.shape, output.stride(), output.dtype),
+                torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else None)
+
+    def _prepare(self, q, q_pe, kv, k_pe, output):
+        """Validate one call's tensors and fill the C arguments for them (output fields aside)."""
         B, H, L = self.batch, self.heads, self.kv_ctx
         for t, name, shape in ((q, "q", (B, H, DIM)), (q_pe, "q_pe", (B, H, PE_DIM)),
                                (kv, "kv", (B, L, 1, DIM)), (k_pe, "k_pe", (B, L, 1, PE_DIM))):
@@ -78,10 +88,8 @@ class MlaKernel:
                 raise ValueError(f"{name} must have unit stride in its last dim")
         if q.dtype not in _DTYPES:
             raise ValueError("dtype must be float16 or bfloat16")
-        ret = output is None
-        if output is None:
-            output = torch.empty(B, H, DIM, dtype=q.dtype, device=q.device)
-        elif tuple(output.shape) != (B, H, DIM) or output.dtype != q.dtype or output.stride(-1) != 1:
+        if output is not None and (tuple(output.shape) != (B, H, DIM) or output.dtype != q.dtype
+                                   or output.stride(-1) != 1):
             raise ValueError("output must be [B, H, 512] in the input dtype")
         seqlens, sched, nsplits = self._schedule(q.device)
         lib = _lib.load()
@@ -105,10 +113,30 @@ class MlaKernel:
         a.cache_seqlens = seqlens.data_ptr()
         a.tile_sched = sched.data_ptr()
         a.num_splits = nsplits.data_ptr()
-        a.out = output.data_ptr()
-        a.o_stride_b, a.o_stride_s, a.o_stride_h = output.stride(0), 0, output.stride(1)
         a.lse = None
         a.workspace = ws.data_ptr()
         a.workspace_bytes = ws.numel()
-        check("mla_decode_fwd", lib.mla_decode_fwd(ctypes.byref(a), _stream_ptr(q.device)))
+        # one split per sequence: the split-KV pass writes every output row, no combine
+        fn = lib.mla_splitkv_fwd if self.splits == 1 else lib.mla_decode_fwd
+        name = "mla_splitkv_fwd" if self.splits == 1 else "mla_decode_fwd"
+        return a, ctypes.byref(a), fn, name, ws
+
+    def __call__(self, q: torch.Tensor, q_pe: torch.Tensor, kv: torch.Tensor, k_pe: torch.Tensor,
+                 output: Optional[torch.Tensor] = None):
+        # A repeat call on the same tensors (the reference's timing loops, a serving loop) only
+        # sets the output pointer and launches: the arguments were validated and filled when
+        # the key was first seen.
+        key = self._key(q, q_pe, kv, k_pe, output)
+        prep = self._prepared if self._prepared is not None and self._prepared[0] == key else None
+        if prep is None:
+            prep = (key, self._prepare(q, q_pe, kv, k_pe, output))
+            self._prepared = prep
+        a, ref, fn, name, _ws = prep[1]
+        ret = output is None
+        if ret:
+            output = torch.empty(self.batch, self.heads, DIM, dtype=q.dtype, device=q.device)
+        a.out = output.data_ptr()
+        a.o_stride_b, a.o_stride_s, a.o_stride_h = output.stride(0), 0, output.stride(1)
+        st = prep[0][2]
+        check(name, fn(ref, st))
         return output if ret else None

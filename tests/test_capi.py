@@ -35,7 +35,7 @@ def test_exports_every_declared_symbol(lib):
     assert sorted(_lib.EXPORTED) == declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.mla_version() == 1
+    assert lib.mla_version() == 2
     assert lib.mla_last_error() is not None
 
 
@@ -110,6 +110,32 @@ def test_workspace_bytes(lib):
     assert lib.mla_workspace_bytes(0, 1, 16, 4) == 0
 
 
+@pytest.mark.parametrize("ramp", ["batch_1_to_256", "random", "tiny_steps"])
+def test_workspace_growth_keeps_retired_below_live(lib, ramp):
+    """A stream's workspace is never freed once handed out, so the buffers it outgrows stay
+    alive: their total must stay below the live buffer's size whatever the request sequence
+    (a batch ramp at H = 128, random sizes, requests one byte apart)."""
+    from mlc_decode_amd.api import grown_workspace_size
+    rng = random.Random(7)
+    if ramp == "batch_1_to_256":
+        needs = [lib.mla_workspace_bytes(b, 1, 128, 256 // 1) + 256 for b in range(1, 257)]
+    elif ramp == "random":
+        needs = [rng.randrange(256, 1 << 34) for _ in range(2000)]
+    else:
+        needs = list(range(300, 5000))
+    live, retired, grown = None, 0, 0
+    for need in needs:
+        if live is None or live < need:
+            size = grown_workspace_size(live, need)
+            assert size >= need and (live is None or size >= 2 * live)
+            if live is not None:
+                retired += live
+            live, grown = size, grown + 1
+            assert retired < live
+    # the ramp of 256 batch sizes reallocates only a handful of times
+    assert grown <= 64 if ramp != "batch_1_to_256" else grown <= 10
+
+
 @pytest.mark.parametrize("ptrs, ns, needle", [
     ((0, 256, 256, 256, 256, 256, 256), 4, b"NULL"),
     ((256,) * 7, 0, b"ns must be in [1, 128]"),
@@ -159,7 +185,7 @@ def _valid_args():
     a.kv_nope, a.kv_rope = base, base + 1024
     a.kv_stride_page = a.kv_rope_stride_page = 64 * 576
     a.kv_stride_tok = a.kv_rope_stride_tok = 576
-    a.block_table, a.block_table_stride = base, 2
+    a.block_table, a.block_table_stride, a.block_table_width = base, 2, 2
     a.num_parts = 4
     a.cache_seqlens = a.tile_sched = a.num_splits = base
     a.out = base
@@ -180,6 +206,13 @@ def _valid_args():
     ("num_parts", 0, 1, b"num_parts"),
     ("sm_scale", 0.0, 1, b"sm_scale"),
     ("workspace_bytes", 0, 2, b"workspace"),
+    # the decode is bounded by the block table's width: it must be given, and
+    # name columns inside one row
+    ("block_table_width", 0, 1, b"block_table_width"),
+    ("block_table_width", 3, 1, b"block_table_width"),
+    ("block_table_width", -1, 1, b"block_table_width"),
+    ("table_reserved", 1, 1, b"table_reserved"),
+    ("status", (1 << 20) + 2, 1, b"status"),
 ])
 def test_decode_rejects_bad_args(lib, field, value, code, needle):
     a = _valid_args()

@@ -35,4 +35,4 @@ def test_tune_cli_records(gpu, tmp_path, capsys):
         assert [r["num_split"] for r in got] == [c["num_split"] for c in cands]
         assert all(r["latency_us"] > 0 for r in got)
         assert best[str(ctx)]["latency_us"] == min(r["latency_us"] for r in got)
-    assert "saved" in capsys.readouterr().out
+    assert "wrote" in capsys.readouterr().out

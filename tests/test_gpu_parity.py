@@ -172,6 +172,47 @@ def test_empty_sequence_and_nan_padding(gpu):
     assert torch.all(out[~good].float() == 0) and torch.all(lse[~good].cpu() == -math.inf)
 
 
+@pytest.mark.parametrize("H,s_q,splits", [(16, 1, None), (16, 1, 1), (128, 1, None), (64, 2, 3)])
+def test_length_past_block_table_width(gpu, H, s_q, splits):
+    """A cache_seqlens entry longer than the block table's row (64 * width tokens) is cut to
+    the row: no column at or past the width is read, and the status word is raised.  The
+    table is a view of the first P columns of a wider tensor whose later columns name pages
+    full of NaN, so a read past the width would poison the output; the last sequence is the
+    over-long one too, where a read past the row would leave the allocation."""
+    P = 6
+    lengths = [64 * P + 100, 64 * P, 200, 64 * P + 1]
+    B = len(lengths)
+    cfg = small_cfg(f"width_h{H}", B, s_q, H, [min(L, 64 * P) for L in lengths])
+    inp = make_inputs(cfg, seed=31 + H)
+    nb = inp.kv_cache.shape[0]
+    poison = torch.full((4, 64, 1, 576), float("nan"), dtype=inp.kv_cache.dtype)
+    kv = torch.cat([inp.kv_cache, poison])
+    wide = torch.full((B, P + 4), nb, dtype=torch.int32)
+    wide[:, P:] = torch.arange(nb, nb + 4, dtype=torch.int32)
+    wide[:, :P] = inp.block_table[:, :P]
+    say(f"length past the block table: H={H} s_q={s_q} splits={splits}")
+    d = inp.to(gpu)
+    kv_d = kv.to(gpu)
+    table = wide.to(gpu)[:, :P]
+    assert table.stride(0) == P + 4 and table.shape[1] == P
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    seqlens = torch.tensor(lengths, dtype=torch.int32, device=gpu)
+    out, lse = mla_decode_with_kvcache(d.q, kv_d, table, seqlens, num_splits=splits,
+                                       sm_scale=inp.sm_scale, causal=True, status=status)
+    torch.cuda.synchronize()
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                  inp.sm_scale, True)
+    assert_parity(out, lse, ref_o, ref_l, "past the table width")
+    assert int(status.item()) == 1
+    # the same batch within bounds leaves the status alone
+    status.zero_()
+    out2, lse2 = mla_decode_with_kvcache(d.q, kv_d, table, d.cache_seqlens, num_splits=splits,
+                                         sm_scale=inp.sm_scale, causal=True, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    assert_parity(out2, lse2, ref_o, ref_l, "within the table width")
+
+
 @pytest.mark.parametrize("H", [16, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_reference_fallback_pass(gpu, H, dtype):
@@ -233,11 +274,13 @@ def test_multi_split_outputs_in_2_4(gpu, H):
 
 @pytest.mark.parametrize("H,dtype", [(16, torch.bfloat16), (16, torch.float16), (128, torch.bfloat16)])
 def test_many_splits_per_sequence(gpu, H, dtype):
-    """Sequences split 9 to 300 ways, against the oracle: the combine's prefetching merges (groups
-    of partial rows in flight, surplus reads past the last split zeroed; 2 groups of 4 when the
-    batch is large next to the part count, 3 groups of 16 when it is small), every count leaving
-    a partial last group, and the plain merge past 256 splits.  The short sequence has fewer
-    pages than splits, so many of its splits are empty (lse = -inf)."""
+    """Sequences split 9 to 300 ways, against the oracle: the combine's general merge (rows of
+    more than 8 splits, four rows per workgroup) and its dim-quarter form for long merges
+    (16 or more parts per sequence: a register queue of 32 partial rows, surplus reads past the
+    last split zeroed), with counts that leave a partial last round of the queue, and the plain
+    merge past 256 splits.  Forced splits give min(splits, pages) non-empty page ranges, so
+    every split here holds keys; splits without a visible key are covered by
+    test_split_with_no_visible_key."""
     cfg = small_cfg(f"many_h{H}", 2, 1, H, [16384, 4001], dtype)
     inp = make_inputs(cfg, seed=40 + H)
     ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
@@ -246,6 +289,23 @@ def test_many_splits_per_sequence(gpu, H, dtype):
         say(f"many splits H={H} dtype={dtype} num_splits={ns}")
         out, lse = run_paged(inp, gpu, ns)
         assert_parity(out, lse, ref_o, ref_l, f"many splits H={H} ns={ns}")
+
+
+@pytest.mark.parametrize("B,L,ns", [(1, 64 * 7 + 1, 8), (1, 64 * 63 + 1, 64), (2, 64 * 11 + 1, 12)])
+def test_split_with_no_visible_key(gpu, B, L, ns):
+    """Causal s_q = 2 where the last split is one page holding only the last token: query 0
+    sees no key of that split, so its partial has lse = -inf there, and the merge must give it
+    weight 0.  Covers the few-splits merge (8 splits), the dim-quarter merge (64 splits, one
+    sequence: 16 or more parts per sequence) and the general one (12 splits, two sequences)."""
+    cfg = small_cfg(f"noviskey_{ns}", B, 2, 16, [L] * B)
+    inp = make_inputs(cfg, seed=ns)
+    ref_o, ref_l = R.decode_paged(inp.q, inp.kv_cache, inp.block_table, inp.cache_seqlens,
+                                  inp.sm_scale, True)
+    say(f"split without a visible key: L={L} num_splits={ns}")
+    out, lse = run_paged(inp, gpu, ns)
+    _, splits = get_mla_metadata(inp.cache_seqlens.to(gpu), 32, 1, forced_splits=ns)
+    assert int(splits[1].item()) == ns  # one split per page at the end: the last holds one token
+    assert_parity(out, lse, ref_o, ref_l, f"no visible key L={L} ns={ns}")
 
 
 def _handmade_runner():
@@ -395,6 +455,16 @@ def test_reference_contiguous_layout(gpu, kv_ctx, monkeypatch):
         kern(*args, out)
         torch.cuda.synchronize()
         assert_parity(out, None, ref, None, f"{name} ctx={kv_ctx}")
+        # repeat calls reuse the prepared arguments: same tensors into a second output, a
+        # returned output, then new input tensors (a changed key), each checked
+        out2 = torch.empty_like(args[0])
+        kern(*args, out2)
+        out3 = kern(*args)
+        fresh = [t.clone() for t in args]
+        out4 = torch.empty_like(args[0])
+        kern(*fresh, out4)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, out) and torch.equal(out3, out) and torch.equal(out4, out)
     assert_parity(baseline_mla.ref_program(*args), None, ref, None, "ref_program")
 
 
