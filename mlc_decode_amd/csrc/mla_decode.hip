@@ -100,6 +100,9 @@ struct KParams {
   int64_t pool_tokens;
   int32_t batch, s_q, heads, rows, causal, num_parts;
   float scale_log2;  // sm_scale * log2(e)
+  // latent and rope halves of one cache tensor (kv_rope = kv_nope + 512, same strides): the
+  // wide kernel then reads a row's rope from its latent address + 1024 bytes
+  int32_t rope_fused;
   // wide kernel, 1-D grid of num_parts * xcd_hb workgroups (a multiple of 8): XCD x runs a
   // contiguous block of parts, the xcd_hb head blocks of a part in consecutive slots
   // (0: a (part, head block) grid)
@@ -254,18 +257,21 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
       : "memory", "m0");
 }
 // The same copy with the LDS destination given as an SGPR plus an immediate (one SALU op,
-// written straight into M0): the wide kernel's stage loads, which step the global address in
-// the per-lane offset instead of the SGPR base (the instruction's immediate offset would move
-// the LDS address too), so a load costs one scalar instruction.  Without the non-temporal
-// hint: workgroups that stream the same pages (the head blocks of a part, neighbouring splits)
-// find them in L2 (measured: 12% fewer fetched bytes at 256 rows, 9% faster at 64 rows).
-template <int LDS_OFF>
+// written straight into M0) and the global address stepped by the instruction's immediate
+// offset GOFF: the wide kernel's stage loads.  The immediate offset moves the LDS destination
+// too (LDS address = M0 + offset + 16 * lane), so M0 takes LDS_OFF - GOFF and the copy lands
+// at lds_base + LDS_OFF; a load then costs one scalar instruction and no vector one.  Without
+// the non-temporal hint: workgroups that stream the same pages (the head blocks of a part,
+// neighbouring splits) find them in L2 (measured: 12% fewer fetched bytes at 256 rows, 9%
+// faster at 64 rows).
+template <int LDS_OFF, int GOFF = 0>
 __device__ __forceinline__ void dma16_m0(uint64_t sbase, uint32_t voff, uint32_t lds_base) {
+  static_assert(GOFF >= 0 && GOFF < 4096 && LDS_OFF - GOFF > -65536, "immediate offset range");
   asm volatile(
       "s_add_u32 m0, %2, %3\n\t"
-      "global_load_lds_dwordx4 %0, %1"
+      "global_load_lds_dwordx4 %0, %1 offset:%4"
       :
-      : "v"(voff), "s"(sbase), "s"(lds_base), "i"(LDS_OFF)
+      : "v"(voff), "s"(sbase), "s"(lds_base), "i"(LDS_OFF - GOFF), "i"(GOFF)
       : "memory", "m0", "scc");
 }
 // The same copy from a per-lane 64-bit address (the sparse path: every token row has its own
@@ -1572,7 +1578,10 @@ constexpr int kLatStageBytes = 32 * 1024;    // 32 token rows x 512 dims
 constexpr int kRopeStageBytes = 4 * 1024;    // 32 token rows x 64 dims
 constexpr int kWidePanel = 16 * 1024;        // tokens 16..31 of a latent stage
 
-template <int DT, int HT>
+// FUSED: the latent and rope halves are one tensor (KParams::rope_fused), so a stage's rope rows
+// are read from the latent row addresses + 1024 bytes (no second page lookup per stage), and
+// each lane holds its page's 64-bit byte offset instead of its page id.
+template <int DT, int HT, bool FUSED>
 __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   constexpr int NW = 4;
   constexpr int RT = NW * HT;        // 16-row tiles per workgroup
@@ -1635,16 +1644,17 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   struct LaneOffsets {
     int kl0, kl1, kr0, kr1, v;
   };
+  // The chunks 2g and 2g + 1 of a row differ in bit 0, which the swizzle leaves in place, so
+  // kl1 = kl0 ^ 16 and kr1 = kr0 ^ 16; kr0 is kl0 with its row-group bit (8 KiB) moved to 1 KiB.
   auto lane_offsets = [&](int ln) __attribute__((always_inline)) {
     const int gg = ln >> 4, ll = ln & 15;
     const int sw0 = (((ll & 7) << 3) + ((2 * gg) ^ stage_swz(ll))) << 4;
-    const int sw1 = (((ll & 7) << 3) + ((2 * gg + 1) ^ stage_swz(ll))) << 4;
     const int r = 4 * gg + (ll >> 2);
     LaneOffsets o;
     o.kl0 = (ll >> 3) * 8192 + sw0;
-    o.kl1 = (ll >> 3) * 8192 + sw1;
+    o.kl1 = o.kl0 ^ 16;
     o.kr0 = (ll >> 3) * 1024 + sw0;
-    o.kr1 = (ll >> 3) * 1024 + sw1;
+    o.kr1 = o.kr0 ^ 16;
     o.v = (r >> 3) * 8192 + ((r & 7) << 7) + ((((ll >> 1) & 1) ^ stage_swz(r)) << 4) + ((ll & 1) << 3) + 2048 * wave;
     return o;
   };
@@ -1671,6 +1681,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     const bool paged = __builtin_amdgcn_readfirstlane(paged_i) != 0;
 
     int pbase = 0, bt_lane = 0;
+    uint32_t pofs_lo = 0, pofs_hi = 0;  // FUSED: byte offset of page pbase + lane in the cache
 
     // page ids pbase .. pbase + 63 of the sequence, one per lane, clamped into the pool
     auto load_page_ids = [&](int first) __attribute__((always_inline)) {
@@ -1680,6 +1691,11 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         const int pi = pbase + lane < last ? pbase + lane : last;
         const int v = p.block_table[(int64_t)b * p.bt_stride + pi];
         bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
+        if constexpr (FUSED) {
+          const uint64_t o = (uint64_t)(uint32_t)bt_lane * (uint32_t)p.kv_sp * 2;
+          pofs_lo = (uint32_t)o;
+          pofs_hi = (uint32_t)(o >> 32);
+        }
       }
     };
     // ---- query fragments of this wave's rows (B operand of S^T = K Q^T), resident for the
@@ -1733,7 +1749,14 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
       const int tok = (st & 1) * kStageTok;
       const char* nb;
       const char* rb;
-      if (paged) {
+      if (paged && FUSED) {
+        const int pidx = st >> 1;
+        if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)pofs_lo, pidx - pbase);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)pofs_hi, pidx - pbase);
+        nb = (const char*)p.kv_nope + ((((uint64_t)hi << 32) | lo) + (uint32_t)(tok * kv_st) * 2);
+        rb = nb;  // unused: the rope load reads nb + 1024
+      } else if (paged) {
         const int pidx = st >> 1;
         if (pidx - pbase >= 64) load_page_ids(pidx);  // uniform
         const uint32_t pg = (uint32_t)__builtin_amdgcn_readlane(bt_lane, pidx - pbase);
@@ -1749,14 +1772,14 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
                (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
       };
       si.nb = uni64(nb);
-      si.rb = uni64(rb);
+      si.rb = FUSED ? si.nb : uni64(rb);
       const int left = L - st * kStageTok;
       const int last_row = (left < kStageTok ? left : kStageTok) - 1;
       int row = 8 * wave + (lane >> 3);
       row = row < last_row && real ? row : last_row;
       const uint32_t cl = real ? (uint32_t)(((lane & 7) ^ stage_swz(((wave & 1) << 3) | (lane >> 3))) << 4) : 0u;
       si.on = (uint32_t)(row * kv_st) * 2 + cl;
-      si.orp = (uint32_t)(row * kr_st) * 2 + cl;
+      si.orp = FUSED ? si.on : (uint32_t)(row * kr_st) * 2 + cl;
       si.lat_dst = (uint32_t)__builtin_amdgcn_readfirstlane(
           (int)(uint32_t)(uintptr_t)(lat + (k % kWideLat) * kLatStageBytes + wave * 8 * 1024));
       si.rope_dst = (uint32_t)__builtin_amdgcn_readfirstlane(
@@ -1765,7 +1788,8 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     };
     auto issue_one = [&](const StageIssue& si, auto jtag) __attribute__((always_inline)) {
       constexpr int j = decltype(jtag)::value;
-      if constexpr (j < 8) dma16_m0<j * 1024>(si.nb, si.on + 128 * j, si.lat_dst);
+      if constexpr (j < 8) dma16_m0<j * 1024, 128 * j>(si.nb, si.on, si.lat_dst);
+      else if constexpr (FUSED) dma16_m0<0, 1024>(si.nb, si.on, si.rope_dst);  // rope = latent row + 1024 B
       else dma16_m0<0>(si.rb, si.orp, si.rope_dst);
     };
     // load j (a constant once the loops around the call are unrolled)
@@ -2024,6 +2048,9 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         }
       }
       // ---- k = 1 .. nst
+      int lnp = lane;
+      asm volatile("" : "+v"(lnp));
+      const LaneOffsets lo_pass = lane_offsets(lnp);
       const int kend = kPV ? nst + 1 : nst;
 #pragma unroll 1
       for (int k = 1; k < kend; ++k) {
@@ -2042,9 +2069,11 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
           if (k >= 3 && wave == 0) over_sh[(k - 2) & 3] = 0;
         }
         const StageIssue si = prepare(k + 2);  // past the segment: dummy loads (see prepare)
+        // 64-row form: from an opaque copy of the lane id per iteration (kept live across the loop
+        // they spill); 128-row form: once per pass (no spill there, 27 fewer VALU per stage)
         int ln = lane;
-        asm volatile("" : "+v"(ln));  // opaque per iteration: the offsets stay inside the loop
-        const LaneOffsets lo = lane_offsets(ln);
+        if constexpr (HT == 1) asm volatile("" : "+v"(ln));
+        const LaneOffsets lo = HT == 1 ? lane_offsets(ln) : lo_pass;
         f32x4 acc[HT][2];
         i32x4 va[WDT];
         if (has_qk) {
@@ -3328,15 +3357,27 @@ bool wide_enabled() {
   return on;
 }
 
-template <int DT, int HT>
-hipError_t launch_wide(const mla::KParams& kp, int head_blocks, hipStream_t st) {
+template <int DT, int HT, bool FUSED>
+void launch_wide_form(const mla::KParams& kp, int head_blocks, hipStream_t st) {
   if ((kp.num_parts * head_blocks) % 8 == 0) {  // XCD-blocked 1-D grid (see the kernel)
     mla::KParams k = kp;
     k.xcd_hb = head_blocks;
-    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT>), dim3(kp.num_parts * head_blocks), dim3(256), 0, st, k);
+    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT, FUSED>), dim3(kp.num_parts * head_blocks), dim3(256), 0, st, k);
   } else {
-    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT>), dim3(kp.num_parts, head_blocks), dim3(256), 0, st, kp);
+    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT, FUSED>), dim3(kp.num_parts, head_blocks), dim3(256), 0, st, kp);
   }
+}
+
+// The fused-rope form for the 128-row kernel only (the 64-row one measured 2% slower with it).
+template <int DT, int HT>
+hipError_t launch_wide(const mla::KParams& kp, int head_blocks, hipStream_t st) {
+  if constexpr (HT == 2) {
+    if (kp.rope_fused) {
+      launch_wide_form<DT, HT, true>(kp, head_blocks, st);
+      return hipGetLastError();
+    }
+  }
+  launch_wide_form<DT, HT, false>(kp, head_blocks, st);
   return hipGetLastError();
 }
 
@@ -3482,6 +3523,12 @@ mla::KParams make_params(const mla_decode_args* a) {
   k.causal = a->causal ? 1 : 0;
   k.num_parts = a->num_parts;
   k.scale_log2 = a->sm_scale * mla::kLog2e;
+  // one cache tensor: the rope half starts 512 elements into each latent row, same strides
+  k.rope_fused = (const uint16_t*)a->kv_rope == (const uint16_t*)a->kv_nope + mla::kDV &&
+                 a->kv_rope_stride_tok == a->kv_stride_tok &&
+                 (a->block_table ? a->kv_rope_stride_page == a->kv_stride_page
+                                 : a->kv_rope_stride_batch == a->kv_stride_batch) &&
+                 a->kv_format == MLA_KV_NATIVE;
   return k;
 }
 
