@@ -156,6 +156,15 @@ __device__ __forceinline__ void qk_settle(f32x4& acc) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc));
 }
 __device__ __forceinline__ void qk_touch(f32x4& acc) { asm volatile("" : "+v"(acc)); }
+// 12 wait states for the QK accumulators when at least eight other MFMAs have issued since the
+// last QK MFMA (20 in all, the most any MFMA result needs before a VALU read).
+template <int HT>
+__device__ __forceinline__ void qk_settle_after_mfmas(f32x4 (&acc)[HT][2]) {
+  if constexpr (HT == 2)
+    asm volatile("s_nop 7\n\ts_nop 3" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
+  else
+    asm volatile("s_nop 7\n\ts_nop 3" : "+v"(acc[0][0]), "+v"(acc[0][1]));
+}
 
 // 32 wait states during which the MFMA source operands passed in stay untouched.
 template <int HT>
@@ -314,16 +323,42 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Lane l's value and lane (l ^ 16)'s, or (l ^ 32)'s, as the two halves of one v_permlane16_swap /
+// v_permlane32_swap of v with itself (lanes 0..31 receive the other row's value in the second
+// half, lanes 32..63 in the first; either way the pair is {v[l], v[l ^ d]}).  No LDS and no lane
+// id: __shfl_xor goes through ds_bpermute with an address formed from the lane id, which the
+// compiler computes once per kernel and, under register pressure, spills; the reload then waits
+// (vmcnt is in order) for every stage load in flight.
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float wave_max_g(float v) {
   // max over the 4 lane groups (lanes l, l^16, l^32, l^48) that hold one row
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  return xor32_max(xor16_max(v));
 }
 __device__ __forceinline__ float wave_sum_g(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  return xor32_sum(xor16_sum(v));
+}
+// The lane id, computed afresh where it is called (two VALU ops the compiler cannot hoist):
+// lane-dependent addresses formed from it stay inside the segment or pass that uses them
+// instead of being computed once per kernel and spilled.
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -535,8 +570,7 @@ __device__ __forceinline__ void wait_lgkm0() {
 // Sequence b's length as the kernels use it: negative lengths read as 0, and a paged sequence
 // longer than its block-table row (64 * bt_width tokens) is cut there, so no column past the
 // table's width is read; that raises the caller's status word (every lane stores the same 1).
-__device__ __forceinline__ int seq_len_bounded(const KParams& p, int b, bool paged) {
-  int L = p.seqlens[b];
+__device__ __forceinline__ int bound_seq_len(const KParams& p, int L, bool paged) {
   L = L > 0 ? L : 0;
   if (paged) {
     const int cap = p.bt_width * kPageTokens;  // bt_width <= 2^24, checked by the host
@@ -546,6 +580,9 @@ __device__ __forceinline__ int seq_len_bounded(const KParams& p, int b, bool pag
     }
   }
   return L;
+}
+__device__ __forceinline__ int seq_len_bounded(const KParams& p, int b, bool paged) {
+  return bound_seq_len(p, p.seqlens[b], paged);
 }
 
 // Waves per SIMD a variant is compiled for: four waves of one 16-row tile each with at most
@@ -666,25 +703,50 @@ void mla_splitkv_kernel(KParams p) {
 #pragma unroll 1
   for (; b < p.batch; ++b, page = 0, split = 0) {
     if (!(b < end_b || (b == end_b && page < end_page))) break;
-    const int L = SPARSE ? p.topk : seq_len_bounded(p, b, paged);
-    const int np = pages_of(L);
-    const int stop = (b == end_b) ? end_page : np;
-    const int st_begin = 2 * page;
-    const int st_end_seq = (L + kStageTok - 1) / kStageTok;
-    const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
-    const int nst = st_end > st_begin ? st_end - st_begin : 0;
+    // Segment prologue: the first 64 page ids, the query fragments and the length are requested
+    // back to back, in that order, so the segment starts after two memory round trips (these
+    // loads, then its first stage) instead of one per dependent load.
+    int pbase = 0, bt_lane = 0;
+    // lane i holds the page id of page (pbase + i), clamped into the pool; the columns read stop
+    // at the table's width, not at the sequence's last page, so the load does not wait for the
+    // length (only the ids of the sequence's own pages are ever used)
+    auto request_page_ids = [&](int first) __attribute__((always_inline)) {
+      pbase = first;
+      if (paged && !SPARSE) {
+        const int last = p.bt_width - 1;
+        const int pi = pbase + lane < last ? pbase + lane : last;
+        bt_lane = p.block_table[(int64_t)b * p.bt_stride + pi];
+      }
+    };
+    auto finish_page_ids = [&]() __attribute__((always_inline)) {
+      if (paged && !SPARSE) {
+        const int v = bt_lane;
+        bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
+      }
+    };
+    auto load_page_ids = [&](int first) __attribute__((always_inline)) {
+      request_page_ids(first);
+      finish_page_ids();
+    };
+    request_page_ids(page);
+    // The sequence's workspace slots, for the epilogue.  The index carries an opaque zero, so
+    // the compiler treats the values as per-lane: it neither moves them into SGPRs (waiting for
+    // them) here nor loads them in the epilogue; they are made uniform where they are used.
+    const int zero_v = fresh_lane() >> 6;
+    const int slot_lo_v = p.splits[b + zero_v];
+    const int slot_hi_v = p.splits[b + 1 + zero_v];
 
     // ---- query fragments (B operand of S^T = K Q^T), resident for the segment.  Rows
     // past the end re-load the last row; their results are never written.
     i32x4 qf[HT][kKSteps];
-    int lim[HT];
+    int qtok[HT];  // query token of each row tile's row
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
       int row = row0 + 16 * ht + li;
       row = row < p.rows ? row : p.rows - 1;
       const int s = row / p.heads;
       const int h = row - s * p.heads;
-      lim[ht] = L - (p.causal ? (p.s_q - 1 - s) : 0);
+      qtok[ht] = s;
       const uint16_t* qn = p.q_nope + (b * p.q_sb + s * p.q_ss + h * p.q_sh) + 16 * g;
       const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 16 * g;
 #pragma unroll
@@ -700,6 +762,20 @@ void mla_splitkv_kernel(KParams p) {
         }
       }
     }
+    // the length and the sequence's workspace slots (loaded here so that the epilogue does not
+    // wait on them) last: awaiting them also awaits everything above (vmcnt is in order), which
+    // is in flight by then
+    const int L = SPARSE ? p.topk : bound_seq_len(p, p.seqlens[b], paged);
+    finish_page_ids();
+    const int np = pages_of(L);
+    const int stop = (b == end_b) ? end_page : np;
+    const int st_begin = 2 * page;
+    const int st_end_seq = (L + kStageTok - 1) / kStageTok;
+    const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
+    const int nst = st_end > st_begin ? st_end - st_begin : 0;
+    int lim[HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) lim[ht] = L - (p.causal ? (p.s_q - 1 - qtok[ht]) : 0);
     const int lmin = L - (p.causal ? p.s_q - 1 : 0);  // every row sees tokens < lmin
     if constexpr (SPARSE) {
       // the segment's index list into LDS (every wave of the workgroup runs this segment; the
@@ -716,19 +792,6 @@ void mla_splitkv_kernel(KParams p) {
     // row sums: l_part of P as rounded for the PV product (normalises the output), l_exact of
     // the fp32 P (gives the lse)
     float m_ref[HT], l_part[HT], l_exact[HT];
-    int pbase = 0, bt_lane = 0;
-
-    auto load_page_ids = [&](int first) __attribute__((always_inline)) {
-      // lane i holds the page id of page (first + i); ids are clamped into the pool
-      pbase = first;
-      if (paged && !SPARSE) {
-        // branch-free: every lane loads an in-bounds entry (row b always has column 0)
-        const int last = np > 0 ? np - 1 : 0;
-        const int pi = pbase + lane < last ? pbase + lane : last;
-        const int v = p.block_table[(int64_t)b * p.bt_stride + pi];
-        bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
-      }
-    };
 
     auto issue = [&](int k) __attribute__((always_inline)) {
       const int st = st_begin + k;
@@ -919,8 +982,10 @@ void mla_splitkv_kernel(KParams p) {
         if (wave == 0) over_sh[lane & 3] = 0;  // uniform branch; ordered by the first barriers
         wait_lgkm0();
       }
-      load_page_ids(page);
-      wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
+      // the first pass uses the page ids loaded in the prologue; a pass after an abort reloads
+      // the window the segment starts in.  The compiler's wait for the ids (and the stage
+      // waits, for the query fragments) count only the loads issued after them.
+      if (pbase != page) load_page_ids(page);  // uniform
 
       if constexpr (NSTAGE == 1) {
         if (k0 < nst) issue(k0);
@@ -1425,8 +1490,8 @@ void mla_splitkv_kernel(KParams p) {
     // padding rows (past the last row) store to the last row: their query was clamped to that
     // row, so they computed bitwise the same values; and all four lane groups of a row store
     // its lse (the same value).
-    const int slot0 = p.splits[b];
-    const bool single = (p.splits[b + 1] - slot0) == 1;
+    const int slot0 = __builtin_amdgcn_readfirstlane(slot_lo_v);
+    const bool single = (__builtin_amdgcn_readfirstlane(slot_hi_v) - slot0) == 1;
     if constexpr (WS) {
       // ---- wave-split merge.  Wave w holds (m_w, l_w, O_w) over its stages (m_w = -inf and
       // l_w = 0 for a wave that had none); the segment's result is
@@ -1624,6 +1689,11 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   constexpr int R = 16 * RT;         // rows per workgroup
   constexpr int WDT = 8;             // 16-dim tiles per wave (128 dims)
   constexpr int DK = 4;              // LDS prefetch depth of the QK A fragments
+  // Three placements in the stage loop that pay at 128 rows per workgroup and cost at 64 (C2 main
+  // kernel 87.7 -> 86.5 us with all three; C5 50.5 -> 49.1 us with none of them at 64 rows):
+  constexpr bool kMaskLate = HT == 2;   // QK results first read inside PV's first step
+  constexpr bool kPtEarly = HT == 2;    // PV's first P^T fragments read at the end of QK
+  constexpr bool kPrepEarly = HT == 2;  // stage k + 2's loads prepared at the end of iteration k - 1
   constexpr float kTau = ref_tau<DT>();
   constexpr int kPBytes = RT * 1024;
   __shared__ __attribute__((aligned(1024))) uint8_t lat_raw[kWideLat * kLatStageBytes];
@@ -1666,9 +1736,9 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   const int end_page = rec[3];
   int split = rec[4];
 
-  // Per-lane LDS offsets of the fragments (recomputed each stage from an opaque copy of the
-  // lane id, see the stage loop: kept live across the loop they get spilled, and a reload
-  // before the loop makes the compiler wait for every outstanding stage load inside it).
+  // Per-lane LDS offsets of the fragments (recomputed from a fresh lane id, see the stage loop:
+  // kept live across the loop they get spilled, and a reload before the loop makes the
+  // compiler wait for every outstanding stage load inside it).
   // QK A operand, fragment (kk, tt), kk < 16: token row 16tt + li of latent chunk
   // sigma(kk, g) = 8*(kk/2) + 2g + kk%2, i.e. block (2tt + li/8)*8 + kk/2, chunk-in-block
   // 2g + kk%2: lane offset kl[kk%2] plus the immediate tt*16 KiB + (kk/2)*1 KiB.  kk = 16, 17:
@@ -1678,7 +1748,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   // segment s; the swizzle flips only address bits 5-6 with d4, so the address is
   // (v_lane ^ 32*d4) + 1024*s.  Wave w's segments are 2w and 2w + 1.
   struct LaneOffsets {
-    int kl0, kl1, kr0, kr1, v;
+    int kl0, kl1, kr0, kr1, v, pt;
   };
   // The chunks 2g and 2g + 1 of a row differ in bit 0, which the swizzle leaves in place, so
   // kl1 = kl0 ^ 16 and kr1 = kr0 ^ 16; kr0 is kl0 with its row-group bit (8 KiB) moved to 1 KiB.
@@ -1692,6 +1762,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     o.kr0 = (ll >> 3) * 1024 + sw0;
     o.kr1 = o.kr0 ^ 16;
     o.v = (r >> 3) * 8192 + ((r & 7) << 7) + ((((ll >> 1) & 1) ^ stage_swz(r)) << 4) + ((ll & 1) << 3) + 2048 * wave;
+    o.pt = 16 * ln;
     return o;
   };
 
@@ -1700,32 +1771,31 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
 #pragma unroll 1
   for (; b < p.batch; ++b, page = 0, split = 0) {
     if (!(b < end_b || (b == end_b && page < end_page))) break;
-    const int L = seq_len_bounded(p, b, p.block_table != nullptr);
-    const int np = pages_of(L);
-    const int stop = (b == end_b) ? end_page : np;
-    const int st_begin = 2 * page;
-    const int st_end_seq = (L + kStageTok - 1) / kStageTok;
-    const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
-    const int nst = st_end > st_begin ? st_end - st_begin : 0;
-    // the sequence's workspace slots, loaded here so that the epilogue does not wait on them
-    const int slot0 = p.splits[b];
-    const bool single = (p.splits[b + 1] - slot0) == 1;
-    // formed per segment from an opaque copy (hoisted, the flag was spilled to scratch and its
-    // reload waited for the query loads in flight)
-    int paged_i = p.block_table != nullptr;
-    asm volatile("" : "+v"(paged_i));
-    const bool paged = __builtin_amdgcn_readfirstlane(paged_i) != 0;
+    // Segment prologue: the first 64 page ids, the query fragments, the length and the split
+    // slots are requested back to back, in that order (nothing waits for the length before it
+    // is requested last), so the segment starts after two memory round trips (these loads,
+    // then its first stage) instead of one per dependent load.
+    const bool paged = p.block_table != nullptr;
 
     int pbase = 0, bt_lane = 0;
     uint32_t pofs_lo = 0, pofs_hi = 0;  // FUSED: byte offset of page pbase + lane in the cache
 
-    // page ids pbase .. pbase + 63 of the sequence, one per lane, clamped into the pool
-    auto load_page_ids = [&](int first) __attribute__((always_inline)) {
+    // page ids pbase .. pbase + 63 of the sequence, one per lane, clamped into the pool.  The
+    // columns read stop at the table's width, not at the sequence's last page, so the load does
+    // not wait for the length; only the ids of the sequence's own pages are ever used.  The
+    // fused form turns them into byte offsets in finish_page_ids, after the other prologue
+    // loads are issued.
+    auto request_page_ids = [&](int first) __attribute__((always_inline)) {
       pbase = first;
       if (paged) {
-        const int last = np > 0 ? np - 1 : 0;
-        const int pi = pbase + lane < last ? pbase + lane : last;
-        const int v = p.block_table[(int64_t)b * p.bt_stride + pi];
+        const int last = p.bt_width - 1;
+        const int pi = pbase + fresh_lane() < last ? pbase + fresh_lane() : last;
+        bt_lane = p.block_table[(int64_t)b * p.bt_stride + pi];
+      }
+    };
+    auto finish_page_ids = [&]() __attribute__((always_inline)) {
+      if (paged) {
+        const int v = bt_lane;
         bt_lane = v < 0 ? 0 : (v >= p.num_blocks ? p.num_blocks - 1 : v);
         if constexpr (FUSED) {
           const uint64_t o = (uint64_t)(uint32_t)bt_lane * (uint32_t)p.kv_sp * 2;
@@ -1734,22 +1804,29 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         }
       }
     };
+    auto load_page_ids = [&](int first) __attribute__((always_inline)) {
+      request_page_ids(first);
+      finish_page_ids();
+    };
     // ---- query fragments of this wave's rows (B operand of S^T = K Q^T), resident for the
     // segment; rows past the end re-load the last row (their results are never written).
-    // The addresses come from an opaque copy of the lane id: otherwise their row-dependent
-    // parts are hoisted out of the segment loop and spilled, and each reload (on the in-order
-    // vmcnt) waits for every load issued before it, a memory round trip apiece.
-    int lq = lane;
-    asm volatile("" : "+v"(lq));
+    // The addresses come from a fresh lane id and an opaque copy of the head count: otherwise
+    // their row-dependent parts (and the reciprocal behind the division by the head count) are
+    // hoisted out of the segment loop and spilled, and each reload (on the in-order vmcnt)
+    // waits for every load issued before it, a memory round trip apiece.
+    request_page_ids(page);
+    const int lq = fresh_lane();
+    int heads_q = p.heads;
+    asm volatile("" : "+s"(heads_q));
     i32x4 qf[HT][kKSteps];
-    int lim[HT];
+    int qtok[HT];  // query token of each row tile's row
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
       int row = row0 + 16 * ht + (lq & 15);
       row = row < p.rows ? row : p.rows - 1;
-      const int s = row / p.heads;
-      const int h = row - s * p.heads;
-      lim[ht] = L - (p.causal ? (p.s_q - 1 - s) : 0);
+      const int s = row / heads_q;
+      const int h = row - s * heads_q;
+      qtok[ht] = s;
       const uint16_t* qn = p.q_nope + (b * p.q_sb + s * p.q_ss + h * p.q_sh) + 16 * (lq >> 4);
       const uint16_t* qr = p.q_rope + (b * p.qr_sb + s * p.qr_ss + h * p.qr_sh) + 16 * (lq >> 4);
 #pragma unroll
@@ -1758,6 +1835,23 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         qf[ht][kk] = *(const i32x4*)(d < kRopeOff ? qn + d : qr + (d - kRopeOff));
       }
     }
+    // the length and the sequence's workspace slots (loaded here so that the epilogue does not
+    // wait on them); awaiting the length also awaits everything above (vmcnt is in order),
+    // which is in flight by then
+    const int l_raw = p.seqlens[b];
+    const int slot0 = p.splits[b];
+    const bool single = (p.splits[b + 1] - slot0) == 1;
+    const int L = bound_seq_len(p, l_raw, paged);
+    finish_page_ids();
+    const int np = pages_of(L);
+    const int stop = (b == end_b) ? end_page : np;
+    const int st_begin = 2 * page;
+    const int st_end_seq = (L + kStageTok - 1) / kStageTok;
+    const int st_end = (2 * stop < st_end_seq) ? 2 * stop : st_end_seq;
+    const int nst = st_end > st_begin ? st_end - st_begin : 0;
+    int lim[HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) lim[ht] = L - (p.causal ? (p.s_q - 1 - qtok[ht]) : 0);
     const int lmin = L - (p.causal ? p.s_q - 1 : 0);  // every row sees tokens < lmin
 
     f32x4 o[WDT][RT];
@@ -1881,8 +1975,10 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
       if constexpr (MODE == kPassFirstStageRef) {
         if (wave == 0) over_sh[lq & 3] = 0;  // uniform branch; ordered by the first barrier
       }
-      load_page_ids(page);
-      wait_vmcnt<0>();  // query fragments and page ids resident before the stage loads start
+      // the first pass uses the page ids loaded in the prologue; a pass after an abort reloads
+      // the window the segment starts in.  The compiler's wait for the ids (and for the query
+      // fragments, before the first MFMA) counts only the loads issued after them.
+      if (pbase != page) load_page_ids(page);  // uniform
       if (0 < nst) issue(0);
       if (1 < nst) issue(1);
 
@@ -1902,14 +1998,21 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         asm volatile("" : "+v"(vb));
         return vb;
       };
+      // P^T fragment rt of stage kp (row tile rt's B operand of PV, one KiB, lane-linear)
+      auto pt_frag = [&](int kp, const LaneOffsets& lo, int rt) __attribute__((always_inline)) {
+        return *(const i32x4 LDS_AS*)(ptb + (kp & 1) * kPBytes + lo.pt + rt * 1024);
+      };
 
       // S^T = K Q^T of stage k over 576 dims: two 16-token tiles x HT row tiles, fragment
       // n = 2*kk + tt, DK fragments in flight.  Loads 0..3 of `si` go out after steps 4, 12, 20
       // and 28; with `vt`, the V^T fragments of stage k-1 are read during the last 8 steps.
       // issue_tag: std::true_type to issue loads 0..3 of `si` between the MFMAs (the stage loop),
       // std::false_type for the peeled first iteration, which has no stage to issue
+      // With `vt`, the first two P^T fragments of stage k-1 (PV's first two steps) are read in
+      // the last steps too, and at 128 rows the QK results are left unsettled: PV's first step
+      // issues eight MFMAs before the softmax reads them (see pv_softmax).
       auto qk = [&](int k, f32x4 (&acc)[HT][2], const LaneOffsets& lo, const StageIssue& si, auto issue_tag,
-                    bool vt, i32x4 (&va)[WDT]) __attribute__((always_inline)) {
+                    bool vt, i32x4 (&va)[WDT], i32x4 (&bq)[2]) __attribute__((always_inline)) {
         const uint8_t LDS_AS* lb = lat + (k % kWideLat) * kLatStageBytes;
         const uint8_t LDS_AS* rbs = rope + (k % kWideRope) * kRopeStageBytes;
         const uint8_t LDS_AS* kb0 = lb + lo.kl0;
@@ -1943,13 +2046,15 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
             if ((n & 7) == 4) issue_j(si, n >> 3);  // loads 0..3
           }
           if (n >= 2 * kKSteps - WDT && vt) va[n - (2 * kKSteps - WDT)] = v_frag(vb, n - (2 * kKSteps - WDT));
+          if (kPtEarly && n >= 2 * kKSteps - 2 && vt) bq[n - (2 * kKSteps - 2)] = pt_frag(k - 1, lo, n - (2 * kKSteps - 2));
           __builtin_amdgcn_sched_barrier(0);
         }
 #undef MLA_WFRAG
-        qk_settle(acc[0][0]);
+        const bool late = kMaskLate && vt;
+        if (!late) qk_settle(acc[0][0]);
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) {
-          if (ht > 0) qk_touch(acc[ht][0]);
+          if (ht > 0 || late) qk_touch(acc[ht][0]);
           qk_touch(acc[ht][1]);
         }
       };
@@ -2002,14 +2107,17 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
 
       // PV of stage kp (O^T += V^T P^T over its 32 tokens: this wave's 8 dim tiles x all RT row
       // tiles) with the softmax of stage kp + 1 and loads 4..8 of `si` woven in.  Step rt
-      // streams P^T fragment rt (two steps ahead) against the 8 resident V^T fragments `va`
-      // (8 MFMAs), then computes two P elements; the slicing is fixed in source order (one
-      // scheduling barrier per step), which also bounds how many operands are live at once.
-      auto pv_softmax = [&](int kp, const f32x4 (&acc)[HT][2], const i32x4 (&va)[WDT],
-                            const StageIssue& si) __attribute__((always_inline)) {
-        const uint8_t LDS_AS* pp = ptb + (kp & 1) * kPBytes + lane * 16;
-        asm volatile("" : "+v"(pp));
-        uint8_t LDS_AS* pw = ptb + ((kp + 1) & 1) * kPBytes + lane * 16;
+      // streams P^T fragment rt (two steps ahead; fragments 0 and 1 come in `bq_in`, read at
+      // the end of QK) against the 8 resident V^T fragments `va` (8 MFMAs), then computes two
+      // P elements; the slicing is fixed in source order (one scheduling barrier per step),
+      // which also bounds how many operands are live at once.  At 128 rows the QK results of
+      // stage kp + 1 are first read after step 0's MFMAs (masking, the row maxima and the
+      // `over` test), so the MFMA pipe goes from QK to PV without a gap; at 64 rows that placement
+      // makes the register allocator spill, and mask_late_in_pv is false.
+      auto pv_softmax = [&](int kp, f32x4 (&acc)[HT][2], const i32x4 (&va)[WDT], const i32x4 (&bq_in)[2],
+                            const StageIssue& si, const LaneOffsets& lo,
+                            bool& over) __attribute__((always_inline)) {
+        uint8_t LDS_AS* pw = ptb + ((kp + 1) & 1) * kPBytes + lo.pt;
         float mu[HT];
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) mu[ht] = m_ref[ht] == -INFINITY ? 0.f : m_ref[ht];
@@ -2029,14 +2137,25 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
           *(i32x4 LDS_AS*)(pw + (wave * HT + ht) * 1024) = pb;
         };
         constexpr int kPer = (8 * HT + RT - 1) / RT;  // P elements per step: 2
-        i32x4 bq[2] = {*(const i32x4 LDS_AS*)pp, *(const i32x4 LDS_AS*)(pp + 1024)};
+        i32x4 bq[2] = {bq_in[0], bq_in[1]};
         i32x4 b_last = bq[0];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           const i32x4 bcur = bq[rt & 1];
-          if (rt + 2 < RT) bq[rt & 1] = *(const i32x4 LDS_AS*)(pp + (rt + 2) * 1024);
+          if (rt + 2 < RT) bq[rt & 1] = pt_frag(kp, lo, rt + 2);
 #pragma unroll
           for (int t = 0; t < WDT; ++t) o[t][rt] = mfma32<DT>(va[t], bcur, o[t][rt]);
+          if (kMaskLate && rt == 0) {
+            // eight MFMAs and 12 more wait states since the last QK MFMA: its results are
+            // readable (the documented need is at most 19 wait states)
+            qk_settle_after_mfmas(acc);
+            float lmx[HT];
+            mask_max(kp + 1, acc, lmx);
+            if constexpr (MODE == kPassFirstStageRef) {
+#pragma unroll
+              for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
+            }
+          }
 #pragma unroll
           for (int q = 0; q < kPer; ++q) {
             const int e = rt * kPer + q;
@@ -2064,12 +2183,11 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         wait_lgkm0();
         lds_barrier();
         if (2 < nst) issue(2);
-        int ln0 = lane;
-        asm volatile("" : "+v"(ln0));
+        const int ln0 = fresh_lane();
         const LaneOffsets lo = lane_offsets(ln0);
         f32x4 acc[HT][2];
-        i32x4 va_unused[WDT];
-        qk(0, acc, lo, StageIssue{}, std::false_type{}, false, va_unused);
+        i32x4 va_unused[WDT], bq_unused[2];
+        qk(0, acc, lo, StageIssue{}, std::false_type{}, false, va_unused, bq_unused);
         float lmx[HT];
         mask_max(0, acc, lmx);
         if constexpr (MODE == kPassRowMax) {
@@ -2084,10 +2202,13 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
         }
       }
       // ---- k = 1 .. nst
-      int lnp = lane;
-      asm volatile("" : "+v"(lnp));
+      const int lnp = fresh_lane();
       const LaneOffsets lo_pass = lane_offsets(lnp);
       const int kend = kPV ? nst + 1 : nst;
+      // the loads of stage k + 2, prepared at the end of iteration k - 1 (while the wave waits
+      // for its P^T stores before the barrier) rather than between the barrier and QK
+      StageIssue si;
+      if constexpr (kPrepEarly) si = prepare(3);
 #pragma unroll 1
       for (int k = 1; k < kend; ++k) {
         const bool has_qk = k < nst;  // uniform
@@ -2104,16 +2225,19 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
           flag_word = over_sh[(k - 1) & 3];
           if (k >= 3 && wave == 0) over_sh[(k - 2) & 3] = 0;
         }
-        const StageIssue si = prepare(k + 2);  // past the segment: dummy loads (see prepare)
-        // 64-row form: from an opaque copy of the lane id per iteration (kept live across the loop
-        // they spill); 128-row form: once per pass (no spill there, 27 fewer VALU per stage)
-        int ln = lane;
-        if constexpr (HT == 1) asm volatile("" : "+v"(ln));
-        const LaneOffsets lo = HT == 1 ? lane_offsets(ln) : lo_pass;
+        if constexpr (!kPrepEarly) si = prepare(k + 2);  // past the segment: dummy loads
+        // 64-row form: from a fresh lane id per iteration (kept live across the loop they
+        // spill); 128-row form: once per pass (no spill there, 27 fewer VALU per stage)
+        const LaneOffsets lo = HT == 1 ? lane_offsets(fresh_lane()) : lo_pass;
         f32x4 acc[HT][2];
         i32x4 va[WDT];
+        i32x4 bq[2];
         if (has_qk) {
-          qk(k, acc, lo, si, std::true_type{}, kPV, va);
+          qk(k, acc, lo, si, std::true_type{}, kPV, va, bq);
+          if constexpr (kPV && !kPtEarly) {
+            bq[0] = pt_frag(k - 1, lo, 0);
+            bq[1] = pt_frag(k - 1, lo, 1);
+          }
         } else {
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht)
@@ -2123,6 +2247,8 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
             const uint8_t LDS_AS* vb = v_base(k - 1, lo);
 #pragma unroll
             for (int t = 0; t < WDT; ++t) va[t] = v_frag(vb, t);
+            bq[0] = pt_frag(k - 1, lo, 0);
+            bq[1] = pt_frag(k - 1, lo, 1);
           }
         }
         if constexpr (MODE == kPassFirstStageRef) {
@@ -2131,24 +2257,28 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
             break;
           }
         }
-        float lmx[HT];
-        mask_max(k, acc, lmx);
-        if constexpr (MODE == kPassRowMax) {
+        bool over = false;
+        if constexpr (!kPV || !kMaskLate) {
+          float lmx[HT];
+          mask_max(k, acc, lmx);
+          if constexpr (MODE == kPassRowMax) {
 #pragma unroll
-          for (int ht = 0; ht < HT; ++ht) m_ref[ht] = fmaxf(m_ref[ht], lmx[ht]);
+            for (int ht = 0; ht < HT; ++ht) m_ref[ht] = fmaxf(m_ref[ht], lmx[ht]);
+          } else if constexpr (MODE == kPassFirstStageRef) {
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
+          }
+        }
+        if constexpr (kPV) {
+          pv_softmax(k - 1, acc, va, bq, si, lo, over);
+        } else {
 #pragma unroll
           for (int j = 4; j < 9; ++j) issue_j(si, j);
-          continue;
         }
-        bool over = false;
-        if constexpr (MODE == kPassFirstStageRef) {
-#pragma unroll
-          for (int ht = 0; ht < HT; ++ht) over |= lmx[ht] > m_ref[ht] + kTau;
-        }
-        if constexpr (kPV) pv_softmax(k - 1, acc, va, si);
         if constexpr (MODE == kPassFirstStageRef) {
           if (__builtin_amdgcn_ballot_w64(over) != 0) over_sh[k & 3] = 1;  // uniform branch
         }
+        if constexpr (kPrepEarly) si = prepare(k + 3);  // past the segment: dummy loads (see prepare)
       }
       wait_vmcnt<0>();  // an abandoned pass may leave stage loads in flight
       wait_lgkm0();
@@ -2168,11 +2298,10 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     // apart from uniform branches; padding rows (past the last row) compute and store the last
     // row's values.
     const int64_t slot = slot0 + split;
-    // Opaque copies of the lane id and the head count: the (row -> token, head) division below
+    // A fresh lane id and an opaque copy of the head count: the (row -> token, head) division below
     // otherwise reuses a constant formed at kernel start, spilled, whose reload in each row
     // tile waits (in-order vmcnt) for every store issued before it.
-    int lane_e = lane;
-    asm volatile("" : "+v"(lane_e));
+    const int lane_e = fresh_lane();
     int heads_e = p.heads;
     asm volatile("" : "+v"(heads_e));
     const int li_e = lane_e & 15, g_e = lane_e >> 4;
@@ -2223,8 +2352,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
 #pragma unroll
         for (int t = 0; t < WDT; ++t) am = fmaxf(am, amax4(o[t][rt]));
         am *= inv;
-        am = fmaxf(am, __shfl_xor(am, 16));
-        am = fmaxf(am, __shfl_xor(am, 32));
+        am = xor32_max(xor16_max(am));
         const int e = part_exp(am);
         const float f = inv * exp2i(e);  // o * (inv * 2^e) rounds exactly as (o * inv) * 2^e
 #pragma unroll
