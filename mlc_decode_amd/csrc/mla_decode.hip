@@ -352,6 +352,12 @@ __device__ __forceinline__ float wave_max_g(float v) {
 __device__ __forceinline__ float wave_sum_g(float v) {
   return xor32_sum(xor16_sum(v));
 }
+// -inf, materialised where it is called (a constant would be hoisted out of a rarely taken branch)
+__device__ __forceinline__ float neg_inf_here() {
+  float v;
+  asm volatile("v_mov_b32 %0, 0xff800000" : "=v"(v));
+  return v;
+}
 // The lane id, computed afresh where it is called (two VALU ops the compiler cannot hoist):
 // lane-dependent addresses formed from it stay inside the segment or pass that uses them
 // instead of being computed once per kernel and spilled.
@@ -2239,10 +2245,14 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
             bq[1] = pt_frag(k - 1, lo, 1);
           }
         } else {
+          // scores of -inf, set inside this branch (as constants the compiler would hoist the
+          // sixteen moves out of it, into every iteration)
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) acc[ht][tt] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[ht][tt][r] = neg_inf_here();
           if constexpr (kPV) {
             const uint8_t LDS_AS* vb = v_base(k - 1, lo);
 #pragma unroll
