@@ -2339,14 +2339,19 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
     // eight full cache lines per instruction.  Stored straight from the fragment layout, each
     // instruction wrote 32-byte pieces of 16 lines, and the store path took ~60 cycles per
     // instruction: ~2000 per row tile.  In the staging rows, 32-byte chunk c of row r sits at
-    // chunk c ^ (r % 8), so the 16 rows of one fragment write fall on 8 chunk positions.
+    // chunk c ^ (r % 8), and its 8-byte piece j (dims 4j .. 4j+3 of the chunk) at piece
+    // j ^ (2 * ((r / 8) % 2)): a fragment write (8 bytes from each of 16 rows, two lane groups
+    // per half-wave) then covers all 64 banks in each half-wave, rows 0-7 of the tile in the
+    // first 16 bytes of their chunks and rows 8-15 in the second.
     uint8_t LDS_AS* const stg = lat + wave * (32 * 1024);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const float inv = inv_sh[16 * rt + li_e];
       const int r = 16 * rt + li_e;  // row of the workgroup
-      // bits 5-7 of the row's LDS address are zero, so the chunk permutation is one XOR
-      const uint32_t srow = (uint32_t)(uintptr_t)(stg + r * 256 + 8 * g_e) ^ (uint32_t)((r & 7) << 5);
+      // bits 3-7 of the row's LDS address are zero, so the chunk and piece permutations are
+      // one XOR
+      const uint32_t srow = (uint32_t)(uintptr_t)(stg + r * 256 + 8 * g_e) ^
+                            (uint32_t)(((r & 7) << 5) | (((r >> 3) & 1) << 4));
       // fragment t holds dims 64*(t%2) + 16*(t/2) + 4g .. +3 of the slice: chunk 4*(t%2) + t/2
       auto put = [&](int t, const i32x2 v) __attribute__((always_inline)) {
         *(i32x2 LDS_AS*)(uintptr_t)(srow ^ (uint32_t)((4 * (t & 1) + (t >> 1)) << 5)) = v;
@@ -2382,7 +2387,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
       const int r0 = lane_e >> 4;
       auto staged = [&](int j) __attribute__((always_inline)) {
         const int r = 4 * j + r0;
-        return *(const i32x4 LDS_AS*)(stg + r * 256 + ((((q >> 1) ^ (r & 7)) << 5) | ((q & 1) << 4)));
+        return *(const i32x4 LDS_AS*)(stg + r * 256 + ((((q >> 1) ^ (r & 7)) << 5) | (((q ^ (r >> 3)) & 1) << 4)));
       };
       // uniform: the workgroup's rows are one run of rows in the destination (no padding rows,
       // one query token), so row r is at a fixed stride from row 0
