@@ -400,13 +400,17 @@ def test_flash_mla_call_shape(gpu):
     assert_parity(out, lse, ref_o, ref_l, "flash_mla")
 
 
-def test_split_latent_rope_views(gpu):
-    cfg = small_cfg("views", 2, 1, 16, [70, 130])
+@pytest.mark.parametrize("H,s_q", [(16, 1), (64, 1), (128, 1), (128, 2)])
+def test_split_latent_rope_views(gpu, H, s_q):
+    """Latent and rope halves in separate allocations: the kernels' general form, where the rope
+    rows are looked up through their own page base (the benchmark caches are one [.., 576]
+    tensor, whose rope half the 64- and 128-row kernels read at the latent row + 1024 bytes)."""
+    cfg = small_cfg(f"views_h{H}_s{s_q}", 2, s_q, H, [70, 130])
     cpu = make_inputs(cfg, seed=12)
     inp = cpu.to(gpu)
     latent = inp.kv_cache[..., :512].contiguous()
     rope = inp.kv_cache[..., 512:].contiguous()
-    say("separate latent / rope tensors")
+    say(f"separate latent / rope tensors: H={H} s_q={s_q}")
     out, lse = mla_decode_with_kvcache(inp.q, (latent, rope), inp.block_table, inp.cache_seqlens)
     ref_o, ref_l = R.decode_paged(cpu.q, cpu.kv_cache, cpu.block_table, cpu.cache_seqlens,
                                   cpu.sm_scale, True)
