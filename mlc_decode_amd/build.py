@@ -1,8 +1,10 @@
 """Build the gfx950 HIP library ``mlc_decode_amd/lib/libmla_decode_amd.so`` in-tree.
 
-One ``hipcc`` invocation compiles the split-KV kernel, the combine kernel, the schedule
-kernel and the C ABI of ``include/mla_decode_amd.h`` into a shared library that
-``mlc_decode_amd._lib`` loads with ctypes.  Runs without a GPU (hipcc cross-compiles).
+``hipcc`` compiles the split-KV kernels, the combine kernel, the schedule kernel and the C ABI
+of ``include/mla_decode_amd.h`` into a shared library that ``mlc_decode_amd._lib`` loads with
+ctypes.  Runs without a GPU (hipcc cross-compiles).  ``csrc/mla_decode_ws.hip`` (the dense
+wave-split kernel) is compiled with LLVM's iterative ILP machine scheduler, every other
+translation unit with the default one.
 """
 from __future__ import annotations
 
@@ -10,6 +12,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -17,10 +20,14 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmla_decode_amd.so")
-SOURCES = [os.path.join(CSRC, "mla_decode.hip")]
+# (source, extra hipcc flags) per translation unit
+SOURCES = [
+    (os.path.join(CSRC, "mla_decode.hip"), []),
+    (os.path.join(CSRC, "mla_decode_ws.hip"), ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]),
+]
 # bench.py's MFMA-rate and shader-clock probe (a measurement helper, not the decode's ABI)
 PROBE_PATH = os.path.join(LIB_DIR, "libmla_probe.so")
-PROBE_SOURCES = [os.path.join(CSRC, "mla_probe.hip")]
+PROBE_SOURCES = [(os.path.join(CSRC, "mla_probe.hip"), [])]
 ARCH = "gfx950"
 
 
@@ -39,24 +46,7 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
-def _compile(sources, target: str, verbose: bool) -> None:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = target + ".tmp"
-    cmd = [
-        hipcc(),
-        f"--offload-arch={ARCH}",
-        "-O3",
-        "-std=c++17",
-        "-fPIC",
-        "-shared",
-        # Packed-FP32 VALU ops are kept out of the generated code (see the repository notes
-        # on gfx950 packed fp32); hipcc's host pass warns that it does not know the feature.
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-I", INCLUDE,
-        "-I", CSRC,
-        "-o", tmp,
-        *sources,
-    ]
+def _run(cmd, verbose: bool) -> None:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
@@ -66,6 +56,30 @@ def _compile(sources, target: str, verbose: bool) -> None:
         for line in (proc.stdout + proc.stderr).splitlines():
             if noise not in line and line.strip():
                 print(line)
+
+
+def _compile(sources, target: str, verbose: bool) -> None:
+    """Compile each (source, flags) unit to an object, then link them into ``target``."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = target + ".tmp"
+    common = [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        # Packed-FP32 VALU ops are kept out of the generated code (see the repository notes
+        # on gfx950 packed fp32); hipcc's host pass warns that it does not know the feature.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", INCLUDE,
+        "-I", CSRC,
+    ]
+    with tempfile.TemporaryDirectory(prefix="mla_build_") as obj_dir:
+        objs = []
+        for i, (src, flags) in enumerate(sources):
+            obj = os.path.join(obj_dir, f"{i}_{os.path.splitext(os.path.basename(src))[0]}.o")
+            _run([hipcc(), *common, *flags, "-c", "-o", obj, src], verbose)
+            objs.append(obj)
+        _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-o", tmp, *objs], verbose)
     os.replace(tmp, target)
 
 
