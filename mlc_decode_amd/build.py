@@ -70,6 +70,9 @@ def _compile(sources, target: str, verbose: bool) -> None:
         # Packed-FP32 VALU ops are kept out of the generated code (see the repository notes
         # on gfx950 packed fp32); hipcc's host pass warns that it does not know the feature.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # scalar kernel arguments arrive preloaded in SGPRs (gfx950 kernarg preloading; the
+        # code object keeps a preamble that loads them where the firmware does not)
+        "-mllvm", "-amdgpu-kernarg-preload-count=16",
         "-I", INCLUDE,
         "-I", CSRC,
     ]

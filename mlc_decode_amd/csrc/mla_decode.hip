@@ -103,10 +103,6 @@ struct KParams {
   // latent and rope halves of one cache tensor (kv_rope = kv_nope + 512, same strides): the
   // wide kernel then reads a row's rope from its latent address + 1024 bytes
   int32_t rope_fused;
-  // wide kernel, 1-D grid of num_parts * xcd_hb workgroups (a multiple of 8): XCD x runs a
-  // contiguous block of parts, the xcd_hb head blocks of a part in consecutive slots
-  // (0: a (part, head block) grid)
-  int32_t xcd_hb;
 };
 
 // ---------------------------------------------------------------------------------------
@@ -612,9 +608,12 @@ constexpr int waves_per_simd(int nw, int ht, int nstage, bool ws) {
 // from LDS to the MFMA, V^T fragments without it, and the scales of V are folded into P^T.
 // SPARSE: the keys of a sequence are the top-k pool tokens its index list names (s_q = 1).
 // (HIP's second launch bound is the minimum number of waves per SIMD, amdgpu_waves_per_eu.)
+// The schedule comes as a scalar argument of its own besides p.sched: the build preloads scalar
+// kernel arguments into SGPRs (-amdgpu-kernarg-preload-count), so the first record load does
+// not wait for the argument segment (a struct argument is never preloaded).
 template <int DT, int NW, int HT, int NSTAGE, bool WS, bool KV8, bool SPARSE = false>
 __global__ __launch_bounds__(NW * 64, waves_per_simd(NW, HT, NSTAGE, WS))
-void mla_splitkv_kernel(KParams p) {
+void mla_splitkv_kernel(const int32_t* __restrict__ sched, KParams p) {
   static_assert(NW == 1 || NW == 4, "one or four waves per workgroup");
   static_assert(!WS || NSTAGE == 1, "wave-split workgroups give each wave a one-stage slot");
   static_assert(!KV8 || DT == MLA_DTYPE_BF16, "the fp8 cache is read with bf16 queries");
@@ -668,7 +667,7 @@ void mla_splitkv_kernel(KParams p) {
   const int k0 = WS ? wave : 0;
   constexpr int kStep = WS ? NW : 1;
 
-  const int32_t* rec = p.sched + part * kSchedWords;
+  const int32_t* rec = sched + part * kSchedWords;
   int b = rec[0];
   int page = rec[1];
   const int end_b = rec[2];
@@ -1688,8 +1687,13 @@ constexpr int kWidePanel = 16 * 1024;        // tokens 16..31 of a latent stage
 // FUSED: the latent and rope halves are one tensor (KParams::rope_fused), so a stage's rope rows
 // are read from the latent row addresses + 1024 bytes (no second page lookup per stage), and
 // each lane holds its page's 64-bit byte offset instead of its page id.
+// sched: p.sched, preloaded (see mla_splitkv_kernel).  xcd_hb > 0: a 1-D grid of num_parts *
+// xcd_hb workgroups (a multiple of 8), xcd_slots = its size / 8; XCD x runs a contiguous block
+// of parts, the xcd_hb head blocks of a part in consecutive slots.  xcd_hb = 0: a (part, head
+// block) grid.  Both are preloaded arguments too: the part index needs them before the record.
 template <int DT, int HT, bool FUSED>
-__global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
+__global__ __launch_bounds__(256, 1) void mla_wide_kernel(const int32_t* __restrict__ sched, int xcd_hb, int xcd_slots,
+                                                          KParams p) {
   constexpr int NW = 4;
   constexpr int RT = NW * HT;        // 16-row tiles per workgroup
   constexpr int R = 16 * RT;         // rows per workgroup
@@ -1719,11 +1723,11 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   // one sequence: consecutive parts) and the same pages (the head blocks of one part) run on
   // one XCD, together, and share its L2.
   int part, hb;
-  if (p.xcd_hb > 0) {
+  if (xcd_hb > 0) {
     const int L = blockIdx.x;
-    const int slot = (L & 7) * (int)(gridDim.x >> 3) + (L >> 3);
-    hb = slot % p.xcd_hb;
-    part = slot / p.xcd_hb;
+    const int slot = (L & 7) * xcd_slots + (L >> 3);
+    hb = xcd_hb == 1 ? 0 : slot % xcd_hb;
+    part = xcd_hb == 1 ? slot : slot / xcd_hb;
   } else {
     part = blockIdx.x;
     hb = blockIdx.y;
@@ -1735,7 +1739,7 @@ __global__ __launch_bounds__(256, 1) void mla_wide_kernel(KParams p) {
   const int rowb = hb * R;                 // the workgroup's first row (PV rows rowb .. +R)
   const int row0 = rowb + wave * 16 * HT;  // this wave's QK rows
 
-  const int32_t* rec = p.sched + part * kSchedWords;
+  const int32_t* rec = sched + part * kSchedWords;
   int b = rec[0];
   int page = rec[1];
   const int end_b = rec[2];
@@ -2441,7 +2445,7 @@ hipError_t launch_ws_dense(const KParams& kp, int head_blocks, hipStream_t st);
 template <int DT>
 hipError_t launch_ws_dense(const KParams& kp, int head_blocks, hipStream_t st) {
   hipLaunchKernelGGL((mla_splitkv_kernel<DT, 4, 1, 1, true, false, false>), dim3(kp.num_parts, head_blocks),
-                     dim3(4 * 64), 0, st, kp);
+                     dim3(4 * 64), 0, st, kp.sched, kp);
   return hipGetLastError();
 }
 template hipError_t launch_ws_dense<MLA_DTYPE_BF16>(const KParams&, int, hipStream_t);
@@ -3540,7 +3544,7 @@ int64_t ws_scale_bytes(int64_t slots, int64_t rows) {
 template <int DT, int NW, int HT, int NS, bool WS, bool KV8 = false, bool SPARSE = false>
 hipError_t launch_main(const mla::KParams& kp, int head_blocks, hipStream_t st) {
   hipLaunchKernelGGL((mla::mla_splitkv_kernel<DT, NW, HT, NS, WS, KV8, SPARSE>), dim3(kp.num_parts, head_blocks),
-                     dim3(NW * 64), 0, st, kp);
+                     dim3(NW * 64), 0, st, kp.sched, kp);
   return hipGetLastError();
 }
 
@@ -3558,12 +3562,13 @@ bool wide_enabled() {
 
 template <int DT, int HT, bool FUSED>
 void launch_wide_form(const mla::KParams& kp, int head_blocks, hipStream_t st) {
-  if ((kp.num_parts * head_blocks) % 8 == 0) {  // XCD-blocked 1-D grid (see the kernel)
-    mla::KParams k = kp;
-    k.xcd_hb = head_blocks;
-    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT, FUSED>), dim3(kp.num_parts * head_blocks), dim3(256), 0, st, k);
+  const int wgs = kp.num_parts * head_blocks;
+  if (wgs % 8 == 0) {  // XCD-blocked 1-D grid (see the kernel)
+    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT, FUSED>), dim3(wgs), dim3(256), 0, st, kp.sched, head_blocks, wgs / 8,
+                       kp);
   } else {
-    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT, FUSED>), dim3(kp.num_parts, head_blocks), dim3(256), 0, st, kp);
+    hipLaunchKernelGGL((mla::mla_wide_kernel<DT, HT, FUSED>), dim3(kp.num_parts, head_blocks), dim3(256), 0, st, kp.sched,
+                       0, 0, kp);
   }
 }
 
