@@ -46,16 +46,20 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
-def _run(cmd, verbose: bool) -> None:
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+def _check(returncode: int, out: str, verbose: bool) -> None:
+    if returncode != 0:
+        sys.stderr.write(out)
+        raise RuntimeError(f"hipcc failed with exit code {returncode}")
     if verbose:
         noise = "is not a recognized feature for this target"
-        for line in (proc.stdout + proc.stderr).splitlines():
+        for line in out.splitlines():
             if noise not in line and line.strip():
                 print(line)
+
+
+def _run(cmd, verbose: bool) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    _check(proc.returncode, proc.stdout + proc.stderr, verbose)
 
 
 def _compile(sources, target: str, verbose: bool) -> None:
@@ -77,11 +81,15 @@ def _compile(sources, target: str, verbose: bool) -> None:
         "-I", CSRC,
     ]
     with tempfile.TemporaryDirectory(prefix="mla_build_") as obj_dir:
-        objs = []
-        for i, (src, flags) in enumerate(sources):
+        objs, procs = [], []
+        for i, (src, flags) in enumerate(sources):  # the units compile side by side
             obj = os.path.join(obj_dir, f"{i}_{os.path.splitext(os.path.basename(src))[0]}.o")
-            _run([hipcc(), *common, *flags, "-c", "-o", obj, src], verbose)
+            procs.append(subprocess.Popen([hipcc(), *common, *flags, "-c", "-o", obj, src],
+                                          stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True))
             objs.append(obj)
+        results = [(p.communicate()[0], p.returncode) for p in procs]
+        for out, rc in results:
+            _check(rc, out, verbose)
         _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-o", tmp, *objs], verbose)
     os.replace(tmp, target)
 
